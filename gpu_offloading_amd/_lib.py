@@ -1,0 +1,143 @@
+"""ctypes binding of libkvc.so, the C ABI declared in include/kvc.h.
+
+The library is built in-tree (``gpu_offloading_amd/lib/libkvc.so``) by
+``gpu_offloading_amd.build.build_library``.  There is no fallback: if the
+library is missing every op raises ``RuntimeError``.
+
+``torch`` is imported before the library is opened so that libkvc.so binds to
+the HIP runtime torch already loaded (both carry the SONAME
+``libamdhip64.so.7``); streams and device pointers handed over from torch are
+then valid inside the library.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_void_p
+
+LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libkvc.so")
+
+KVC_OK = 0
+STATUS_NAMES = {
+    0: "KVC_OK",
+    1: "KVC_ERR_INVALID_ARG",
+    2: "KVC_ERR_UNSUPPORTED",
+    3: "KVC_ERR_ALIGNMENT",
+    4: "KVC_ERR_WORKSPACE",
+    5: "KVC_ERR_HIP",
+}
+
+
+class KvcDecodeSchedule(ctypes.Structure):
+    """Mirror of ``kvc_decode_schedule`` (include/kvc.h)."""
+
+    _fields_ = [
+        ("batch", c_int32),
+        ("num_qo_heads", c_int32),
+        ("num_kv_heads", c_int32),
+        ("head_dim", c_int32),
+        ("page_size", c_int32),
+        ("pages_per_partition", c_int32),
+        ("max_partitions", c_int32),
+        ("total_pages", c_int32),
+        ("num_empty", c_int32),
+        ("workspace_bytes", c_int64),
+    ]
+
+
+_P = c_void_p
+_I32P = c_void_p  # device int32 pointers are passed as raw addresses
+# name -> (restype, argtypes).  Every entry point of include/kvc.h is listed;
+# tests check this table against the header and the library's exports.
+SIGNATURES = {
+    "kvc_version": (c_int, []),
+    "kvc_status_string": (c_char_p, [c_int]),
+    "kvc_last_error": (c_char_p, []),
+    "kvc_reshape_and_cache_flash": (c_int, [
+        _P, _P, _P, _P, _P,
+        c_int64, c_int32, c_int32, c_int32, c_int64, c_int32,
+        c_int64, c_int64, c_int64, c_int64,
+        _I32P, _P]),
+    "kvc_gather_kv": (c_int, [
+        _P, _P, _I32P, c_int64, c_int32, _I32P, _I32P,
+        c_int32, c_int32, c_int32, c_int32, c_int32, c_int64, c_int32,
+        c_int64, c_int64, _P, _P, c_int64, _I32P, _P]),
+    "kvc_decode_plan": (c_int, [
+        c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+        POINTER(KvcDecodeSchedule)]),
+    "kvc_decode_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32]),
+    "kvc_batch_decode_run": (c_int, [
+        POINTER(KvcDecodeSchedule), _P, c_int64, _P, _P, c_int64, c_int64, c_int64,
+        _I32P, _I32P, c_int64, _I32P, c_float, _P, c_int64, _P, c_int64, _P, _P]),
+    "kvc_merge_attention_states": (c_int, [
+        _P, _P, _P, _P, c_int64, c_int32, _P, _P, _P]),
+    "kvc_gather_blocks": (c_int, [
+        _P, _P, c_int64, c_int64, c_int64, _I32P, c_int64, _P, _I32P, _P]),
+    "kvc_scatter_blocks": (c_int, [
+        _P, _I32P, c_int64, _P, _P, c_int64, c_int64, c_int64, _I32P, _P]),
+    "kvc_swap_out": (c_int, [
+        _P, _P, c_int64, c_int64, c_int64, _I32P, c_int64, _P, c_int64, _P,
+        _I32P, _P]),
+    "kvc_swap_in": (c_int, [
+        _P, _I32P, c_int64, _P, _P, c_int64, c_int64, c_int64, _P, c_int64,
+        _I32P, _P]),
+    "kvc_compute_slot_mapping": (c_int, [
+        _I32P, c_int64, c_int32, c_int32, _I32P, _I32P, _I32P,
+        c_int32, c_int32, c_int32, c_int32, _P, _I32P, _P]),
+    "kvc_copy_page_indices": (c_int, [
+        _I32P, c_int64, c_int32, _I32P, _I32P, c_int32, c_int32, _I32P, _P]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class KvcError(RuntimeError):
+    """A libkvc call returned a non-zero status (raised as RuntimeError, like
+    the TORCH_CHECK failures of the library ops it replaces)."""
+
+    def __init__(self, func: str, status: int, detail: str):
+        self.func = func
+        self.status = status
+        self.detail = detail
+        super().__init__(f"{func} failed with {STATUS_NAMES.get(status, status)}: {detail}")
+
+
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Open libkvc.so once and attach the signatures of include/kvc.h."""
+    global _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        import torch  # noqa: F401  (bind to torch's HIP runtime, see module doc)
+
+        p = path or LIB_PATH
+        if not os.path.exists(p):
+            raise RuntimeError(
+                f"{p} is not built. Build it with "
+                "`python -c 'import __graft_entry__ as g; g.build()'` "
+                "(or gpu_offloading_amd.build.build_library()); "
+                "there is no CPU fallback for the KV-cache ops.")
+        lib = ctypes.CDLL(p, mode=ctypes.RTLD_LOCAL)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def check(func: str, status: int) -> None:
+    if status != KVC_OK:
+        detail = load().kvc_last_error().decode(errors="replace")
+        raise KvcError(func, status, detail)
+
+
+def call(name: str, *args) -> int:
+    """Call an int-status entry point and raise KvcError on failure."""
+    st = getattr(load(), name)(*args)
+    check(name, st)
+    return st

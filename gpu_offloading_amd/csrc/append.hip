@@ -1,0 +1,187 @@
+// (a5) KV append: slot_mapping scatter of new K/V token rows into the paged
+// cache.  Semantics follow vLLM reshape_and_cache_flash as the reference engine
+// calls it (src/MoE/moe_engine.py:2059-2062, "auto" dtype = plain copy, scales
+// unused, slot < 0 = padding) and its PyTorch twin at moe_engine.py:2196-2198.
+//
+// Design: the work unit is one 16-byte chunk of one token's K or V row (a
+// token row is num_kv_heads*head_dim contiguous elements in both the source
+// and the cache).  A 256-thread workgroup owns 256*kUnroll consecutive chunks;
+// each lane issues kUnroll 16-byte loads before its stores so that several
+// global_load_dwordx4 are in flight per lane.  Consecutive lanes touch
+// consecutive 16-byte chunks of the same row, so every load and store
+// instruction is fully coalesced.  Bytes are moved as raw words (bit-exact).
+#include "kvc_common.h"
+
+#include <algorithm>
+
+namespace kvc {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+
+struct AppendArgs {
+  const char* key;
+  const char* value;
+  char* key_cache;
+  char* value_cache;
+  const int64_t* slots;
+  int64_t num_tokens;
+  int64_t key_stride;      // bytes between source tokens
+  int64_t value_stride;
+  int64_t block_stride;    // bytes between cache blocks
+  int64_t token_stride;    // bytes between tokens inside a block
+  int64_t num_slots;       // num_blocks * block_size
+  int32_t block_size;
+  int32_t row_units;       // units (16 B or elem) per token row
+  int32_t* oob_count;
+};
+
+// kRowChunks > 0 fixes the 16-byte chunks per row at compile time (the
+// 8 heads x 128 dims bf16 rows of the reference models have 128).
+template <int kRowChunks>
+__global__ __launch_bounds__(kThreads) void append_vec16_kernel(AppendArgs a) {
+  // The host guarantees num_tokens * per_tok < 2^32, so 32-bit index math.
+  const uint32_t rc = kRowChunks > 0 ? uint32_t(kRowChunks) : uint32_t(a.row_units);
+  const uint32_t per_tok = 2u * rc;
+  const uint32_t total = uint32_t(a.num_tokens) * per_tok;
+  const uint32_t base = blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
+
+  uint4 buf[kUnroll];
+  char* dst[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint32_t item = base + uint32_t(u) * kThreads;
+    dst[u] = nullptr;
+    if (item >= total) continue;
+    const uint32_t tok = item / per_tok;
+    const uint32_t rem = item - tok * per_tok;
+    const bool is_v = rem >= rc;
+    const uint32_t chunk = is_v ? rem - rc : rem;
+    const int64_t slot = a.slots[tok];
+    if (slot < 0) continue;  // padding token
+    if (slot >= a.num_slots) {
+      if (a.oob_count && chunk == 0 && !is_v) atomicAdd(a.oob_count, 1);
+      continue;
+    }
+    const int64_t blk = slot / a.block_size;
+    const int64_t off = slot - blk * a.block_size;
+    const char* src = (is_v ? a.value + int64_t(tok) * a.value_stride
+                            : a.key + int64_t(tok) * a.key_stride) + chunk * 16u;
+    buf[u] = *reinterpret_cast<const uint4*>(src);
+    dst[u] = (is_v ? a.value_cache : a.key_cache) + blk * a.block_stride +
+             off * a.token_stride + chunk * 16u;
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u)
+    if (dst[u]) *reinterpret_cast<uint4*>(dst[u]) = buf[u];
+}
+
+// Fallback for rows that are not a whole number of aligned 16-byte chunks:
+// one element per work item (elem_bytes 1, 2 or 4).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void append_elem_kernel(AppendArgs a) {
+  const uint64_t re = uint64_t(a.row_units);
+  const uint64_t per_tok = 2 * re;
+  const uint64_t total = uint64_t(a.num_tokens) * per_tok;
+  for (uint64_t item = uint64_t(blockIdx.x) * kThreads + threadIdx.x;
+       item < total; item += uint64_t(gridDim.x) * kThreads) {
+    const uint64_t tok = item / per_tok;
+    const uint64_t rem = item - tok * per_tok;
+    const bool is_v = rem >= re;
+    const uint64_t e = is_v ? rem - re : rem;
+    const int64_t slot = a.slots[tok];
+    if (slot < 0) continue;
+    if (slot >= a.num_slots) {
+      if (a.oob_count && e == 0 && !is_v) atomicAdd(a.oob_count, 1);
+      continue;
+    }
+    const int64_t blk = slot / a.block_size;
+    const int64_t off = slot - blk * a.block_size;
+    const T* src = reinterpret_cast<const T*>(
+        (is_v ? a.value + tok * a.value_stride : a.key + tok * a.key_stride));
+    T* dst = reinterpret_cast<T*>((is_v ? a.value_cache : a.key_cache) +
+                                  blk * a.block_stride + off * a.token_stride);
+    dst[e] = src[e];
+  }
+}
+
+}  // namespace
+}  // namespace kvc
+
+using namespace kvc;
+
+extern "C" int kvc_reshape_and_cache_flash(
+    const void* key, const void* value, void* key_cache, void* value_cache,
+    const int64_t* slot_mapping, int64_t num_tokens, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int64_t num_blocks,
+    int32_t elem_bytes, int64_t key_token_stride, int64_t value_token_stride,
+    int64_t cache_block_stride, int64_t cache_token_stride, int32_t* oob_count,
+    void* stream) {
+  KVC_REQUIRE(num_tokens >= 0, KVC_ERR_INVALID_ARG, "num_tokens < 0");
+  if (num_tokens == 0) return ok();
+  KVC_REQUIRE(key && value && key_cache && value_cache && slot_mapping,
+              KVC_ERR_INVALID_ARG, "null pointer");
+  KVC_REQUIRE(num_kv_heads > 0 && head_dim > 0 && block_size > 0 &&
+                  num_blocks > 0,
+              KVC_ERR_INVALID_ARG, "non-positive shape");
+  KVC_REQUIRE(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4,
+              KVC_ERR_UNSUPPORTED, "elem_bytes must be 1, 2 or 4");
+  const int64_t row_elems = int64_t(num_kv_heads) * head_dim;
+  KVC_REQUIRE(key_token_stride >= row_elems && value_token_stride >= row_elems,
+              KVC_ERR_INVALID_ARG, "source token stride smaller than a row");
+  KVC_REQUIRE(cache_token_stride >= row_elems &&
+                  cache_block_stride >= cache_token_stride * block_size,
+              KVC_ERR_INVALID_ARG, "cache strides smaller than the block");
+  KVC_REQUIRE(num_tokens * 2 * row_elems * elem_bytes < (int64_t(1) << 32),
+              KVC_ERR_INVALID_ARG,
+              "more than 4 GiB of K+V rows in one call; split the batch");
+
+  AppendArgs a;
+  a.key = static_cast<const char*>(key);
+  a.value = static_cast<const char*>(value);
+  a.key_cache = static_cast<char*>(key_cache);
+  a.value_cache = static_cast<char*>(value_cache);
+  a.slots = slot_mapping;
+  a.num_tokens = num_tokens;
+  a.key_stride = key_token_stride * elem_bytes;
+  a.value_stride = value_token_stride * elem_bytes;
+  a.block_stride = cache_block_stride * elem_bytes;
+  a.token_stride = cache_token_stride * elem_bytes;
+  a.num_slots = num_blocks * block_size;
+  a.block_size = block_size;
+  a.oob_count = oob_count;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  const int64_t row_bytes = row_elems * elem_bytes;
+  const bool vec = (row_bytes % 16 == 0) && aligned(key, 16) &&
+                   aligned(value, 16) && aligned(key_cache, 16) &&
+                   aligned(value_cache, 16) && a.key_stride % 16 == 0 &&
+                   a.value_stride % 16 == 0 && a.block_stride % 16 == 0 &&
+                   a.token_stride % 16 == 0;
+  if (vec) {
+    a.row_units = int32_t(row_bytes / 16);
+    const int64_t items = num_tokens * 2 * a.row_units;
+    const int64_t grid = (items + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+    if (a.row_units == 128)
+      append_vec16_kernel<128><<<dim3(unsigned(grid)), kThreads, 0, s>>>(a);
+    else
+      append_vec16_kernel<0><<<dim3(unsigned(grid)), kThreads, 0, s>>>(a);
+  } else {
+    KVC_REQUIRE(aligned(key, elem_bytes) && aligned(value, elem_bytes) &&
+                    aligned(key_cache, elem_bytes) &&
+                    aligned(value_cache, elem_bytes),
+                KVC_ERR_ALIGNMENT, "pointers not aligned to elem_bytes");
+    a.row_units = int32_t(row_elems);
+    const int64_t items = num_tokens * 2 * row_elems;
+    const int64_t grid = std::min<int64_t>((items + kThreads - 1) / kThreads, 65536);
+    if (elem_bytes == 2)
+      append_elem_kernel<uint16_t><<<dim3(unsigned(grid)), kThreads, 0, s>>>(a);
+    else if (elem_bytes == 4)
+      append_elem_kernel<uint32_t><<<dim3(unsigned(grid)), kThreads, 0, s>>>(a);
+    else
+      append_elem_kernel<uint8_t><<<dim3(unsigned(grid)), kThreads, 0, s>>>(a);
+  }
+  KVC_LAUNCH_CHECK();
+  return ok();
+}

@@ -1,0 +1,230 @@
+"""Paged GQA decode attention with FlashInfer's wrapper interface.
+
+``BatchDecodeWithPagedKVCacheWrapper`` keeps the constructor / ``plan`` /
+``run`` signature the reference engine uses
+(src/MoE/moe_engine.py:551-552 construct, :1352-1358 and :1949-1955 plan,
+:2069-2070 and :3907-3909 run) and launches the HIP kernels of
+csrc/decode.hip through libkvc.so.
+
+``plan`` is host work (plus small H2D copies), like FlashInfer's: it reads the
+host indptr, picks the split-K partition size and stages indptr / indices /
+last_page_len on the device.  ``run`` launches the partition kernel and, when a
+request spans more than one partition, the merge kernel.  ``plan`` must be
+called again whenever the sequence lengths change (the engine re-plans every
+step after bumping ``_seq_lens_cpu``, moe_engine.py:3554-3556).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple, Union
+
+import torch
+
+from . import _lib
+
+__all__ = ["BatchDecodeWithPagedKVCacheWrapper"]
+
+_DEFAULT_WORKSPACE = 128 * 1024 * 1024  # the engine's FlashInfer workspace (moe_engine.py:541-542)
+
+
+def _fail(msg: str) -> None:
+    raise RuntimeError(msg)
+
+
+class BatchDecodeWithPagedKVCacheWrapper:
+    """Decode attention over a paged KV cache ("NHD" layout).
+
+    Parameters mirror FlashInfer's wrapper.  ``float_workspace_buffer`` is a
+    device byte buffer that holds split-K partials (FlashInfer's engine call
+    passes 128 MiB); ``plan`` raises if a batch needs more.
+    """
+
+    def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD",
+                 use_cuda_graph: bool = False, use_tensor_cores: bool = False,
+                 paged_kv_indptr_buffer: Optional[torch.Tensor] = None,
+                 paged_kv_indices_buffer: Optional[torch.Tensor] = None,
+                 paged_kv_last_page_len_buffer: Optional[torch.Tensor] = None,
+                 pages_per_partition: Optional[int] = None):
+        if kv_layout != "NHD":
+            _fail(f"kv_layout={kv_layout!r} is not supported (only 'NHD')")
+        if not float_workspace_buffer.is_cuda:
+            _fail("float_workspace_buffer must be a GPU tensor")
+        self._workspace = float_workspace_buffer
+        self._device = float_workspace_buffer.device
+        self._use_cuda_graph = use_cuda_graph
+        self._indptr_buf = paged_kv_indptr_buffer
+        self._indices_buf = paged_kv_indices_buffer
+        self._lpl_buf = paged_kv_last_page_len_buffer
+        self._ppp_hint = int(pages_per_partition or 0)
+        self._num_cus = torch.cuda.get_device_properties(self._device).multi_processor_count
+        self._sched: Optional[_lib.KvcDecodeSchedule] = None
+        self._indices = None
+        self._num_indices = 0
+        self._sm_scale = None
+        self._plan_args = None
+
+    # ------------------------------------------------------------------ plan
+    def plan(self, indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
+             num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
+             pos_encoding_mode: str = "NONE", window_left: int = -1,
+             logits_soft_cap: Optional[float] = None,
+             q_data_type: Union[str, torch.dtype] = torch.bfloat16,
+             kv_data_type: Optional[Union[str, torch.dtype]] = None,
+             data_type: Optional[Union[str, torch.dtype]] = None,
+             sm_scale: Optional[float] = None, rope_scale: Optional[float] = None,
+             rope_theta: Optional[float] = None, non_blocking: bool = True) -> None:
+        """Stage the batch metadata and choose the split-K schedule.
+
+        indptr ``[B+1]`` int32 (page offsets), indices ``[indptr[B]]`` int32
+        (physical page ids), last_page_len ``[B]`` int32 (1..page_size tokens
+        in each request's final page).  Host or device tensors are accepted;
+        the schedule is computed from a host copy of indptr.
+        """
+        if pos_encoding_mode != "NONE":
+            _fail(f"pos_encoding_mode={pos_encoding_mode!r} not supported (engine uses 'NONE')")
+        if window_left != -1 or logits_soft_cap not in (None, 0, 0.0):
+            _fail("sliding windows and logits soft-cap are not supported")
+        for dt in (q_data_type, kv_data_type, data_type):
+            if dt is not None and dt not in (torch.bfloat16, "bfloat16", "bf16"):
+                _fail(f"only bfloat16 q/kv are supported, got {dt}")
+        if page_size != 16:
+            _fail("page_size must be 16")
+        if num_qo_heads % num_kv_heads != 0:
+            _fail("num_qo_heads must be a multiple of num_kv_heads")
+        for name, t in (("indptr", indptr), ("indices", indices), ("last_page_len", last_page_len)):
+            if t.dtype != torch.int32:
+                _fail(f"{name} must be int32")
+        batch = indptr.numel() - 1
+        if batch < 0:
+            _fail("indptr must have at least one entry")
+        if last_page_len.numel() < batch:
+            _fail("last_page_len needs one entry per request")
+
+        indptr_host = indptr[: batch + 1].to("cpu").contiguous() if indptr.is_cuda \
+            else indptr[: batch + 1].contiguous()
+        sched = _lib.KvcDecodeSchedule()
+        _lib.call("kvc_decode_plan", indptr_host.data_ptr(), batch, num_qo_heads, num_kv_heads,
+                  head_dim, page_size, self._ppp_hint, self._num_cus, sched)
+        ws = self._workspace.numel() * self._workspace.element_size()
+        if sched.workspace_bytes > ws:
+            _fail(f"decode workspace too small: need {sched.workspace_bytes} bytes, have {ws}")
+        total = int(indptr_host[-1]) if batch > 0 else 0
+        if indices.numel() < total:
+            _fail(f"indices has {indices.numel()} entries, indptr[-1] = {total}")
+
+        dev = self._device
+        # Device copies of indptr / last_page_len, staged through a fresh
+        # pinned tensor: torch's caching host allocator keeps it alive until
+        # the async copy has run, so plan() never waits for the GPU.
+        n_meta = 2 * batch + 1
+        hs = torch.empty(n_meta, dtype=torch.int32, pin_memory=True)
+        hs[: batch + 1].copy_(indptr_host)
+        hs[batch + 1:].copy_(last_page_len[:batch])
+        dm = hs.to(dev, non_blocking=True)
+        if self._indptr_buf is not None:
+            self._indptr_buf[: batch + 1].copy_(dm[: batch + 1])
+            indptr_dev = self._indptr_buf
+        else:
+            indptr_dev = dm[: batch + 1]
+        if self._lpl_buf is not None:
+            self._lpl_buf[:batch].copy_(dm[batch + 1: n_meta])
+            lpl_dev = self._lpl_buf
+        else:
+            lpl_dev = dm[batch + 1: n_meta]
+        if indices.is_cuda:
+            if indices.device != dev:
+                _fail("indices on a different device than the workspace")
+            if self._indices_buf is not None:
+                self._indices_buf[:total].copy_(indices[:total])
+                indices_dev = self._indices_buf
+            else:
+                indices_dev = indices
+        else:
+            host_idx = indices[:total]
+            if not host_idx.is_pinned():
+                host_idx = host_idx.pin_memory()
+            indices_dev = host_idx.to(dev, non_blocking=True)
+        if not indices_dev.is_contiguous():
+            indices_dev = indices_dev.contiguous()
+
+        self._sched = sched
+        self._indptr = indptr_dev
+        self._lpl = lpl_dev
+        self._indices = indices_dev
+        self._num_indices = indices_dev.numel()
+        self._sm_scale = float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(head_dim)
+        self._plan_args = (batch, num_qo_heads, num_kv_heads, head_dim, page_size)
+
+    begin_forward = plan
+
+    @property
+    def schedule(self) -> _lib.KvcDecodeSchedule:
+        return self._sched
+
+    # ------------------------------------------------------------------- run
+    def run(self, q: torch.Tensor,
+            paged_kv_cache: Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]],
+            *args, out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
+            return_lse: bool = False, q_scale: Optional[float] = None,
+            k_scale: Optional[float] = None, v_scale: Optional[float] = None,
+            stream: Optional[torch.cuda.Stream] = None, **kwargs):
+        """Attention of ``q [B, num_qo_heads, head_dim]`` over the planned pages.
+
+        ``paged_kv_cache`` is ``(k_cache, v_cache)`` each
+        ``[num_pages, page_size, num_kv_heads, head_dim]``, or one tensor
+        ``[num_pages, 2, page_size, num_kv_heads, head_dim]``.  Returns ``out``
+        (bf16 ``[B, num_qo_heads, head_dim]``) or ``(out, lse)``; lse is the
+        natural-log log-sum-exp of the scaled logits.
+        """
+        if self._sched is None:
+            _fail("run() called before plan()")
+        if any(s not in (None, 1.0) for s in (q_scale, k_scale, v_scale)):
+            _fail("q/k/v scales are not supported (bf16 cache)")
+        batch, hq, hkv, d, ps = self._plan_args
+        if isinstance(paged_kv_cache, (tuple, list)):
+            k_cache, v_cache = paged_kv_cache
+        else:
+            if paged_kv_cache.dim() != 5 or paged_kv_cache.shape[1] != 2:
+                _fail("a single paged_kv_cache tensor must be [pages, 2, page_size, heads, dim]")
+            k_cache, v_cache = paged_kv_cache[:, 0], paged_kv_cache[:, 1]
+        for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+            if c.dim() != 4 or tuple(c.shape[1:]) != (ps, hkv, d):
+                _fail(f"{name} must be [pages, {ps}, {hkv}, {d}], got {tuple(c.shape)}")
+            if c.dtype != torch.bfloat16:
+                _fail(f"{name} must be bfloat16")
+            if c.stride(3) != 1 or c.stride(2) != d:
+                _fail(f"{name}: heads of a token must be contiguous")
+            if c.device != self._device:
+                _fail(f"{name} on {c.device}, workspace on {self._device}")
+        if k_cache.stride() != v_cache.stride() or k_cache.shape[0] != v_cache.shape[0]:
+            _fail("k_cache and v_cache must share shape and strides")
+        if q.dim() != 3 or q.shape[0] < batch or tuple(q.shape[1:]) != (hq, d):
+            _fail(f"q must be [{batch}, {hq}, {d}], got {tuple(q.shape)}")
+        if q.dtype != torch.bfloat16 or q.stride(2) != 1 or q.stride(1) != d:
+            _fail("q must be bfloat16 with contiguous heads")
+        if q.device != self._device:
+            _fail("q on a different device than the workspace")
+        if out is None:
+            out = torch.empty(batch, hq, d, dtype=torch.bfloat16, device=self._device)
+        elif (out.dtype != torch.bfloat16 or out.dim() != 3 or out.shape[0] < batch
+              or tuple(out.shape[1:]) != (hq, d) or out.stride(2) != 1 or out.stride(1) != d):
+            _fail("out must be bfloat16 [B, num_qo_heads, head_dim] with contiguous heads")
+        if return_lse and lse is None:
+            lse = torch.empty(batch, hq, dtype=torch.float32, device=self._device)
+        if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()
+                                or lse.numel() < batch * hq):
+            _fail("lse must be contiguous float32 [B, num_qo_heads]")
+        s = stream if stream is not None else torch.cuda.current_stream(self._device)
+        ws = self._workspace
+        _lib.call("kvc_batch_decode_run", self._sched, q.data_ptr(), q.stride(0),
+                  k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
+                  k_cache.shape[0], self._indptr.data_ptr(), self._indices.data_ptr(),
+                  self._num_indices, self._lpl.data_ptr(), self._sm_scale, ws.data_ptr(),
+                  ws.numel() * ws.element_size(), out.data_ptr(), out.stride(0),
+                  lse.data_ptr() if lse is not None else None, s.cuda_stream)
+        return (out, lse) if return_lse else out
+
+    forward = run
+
+    def end_forward(self) -> None:
+        """No-op kept for interface parity."""

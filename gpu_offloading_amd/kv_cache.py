@@ -1,0 +1,462 @@
+"""The paged KV cache of the reference MoE engine, MI355X-native.
+
+``PagedKVCache`` is the KV-cache subset of ``MoEEngine``
+(src/MoE/moe_engine.py): the per-layer ``k_cache`` / ``v_cache`` tensors
+(:488-500), the block table (:504-519), ``seq_lens`` with its host mirror
+(:535-539), the dynamic page pool and its API (:578-582, 4185-4297),
+``kv_snapshot`` / ``kv_restore`` / ``fill_kv_random`` (:4152-4183), the slot
+mapping and decode planning of a step (:1896-1955, 3475-3556) and the two
+kernels called per layer: the KV append (:2343-2347) and decode attention
+(:3907-3909).  It also adds the swap API the engine lacks (block eviction to
+pinned host memory and restore, on a side stream).
+
+All arithmetic runs in libkvc.so; this module only does host bookkeeping,
+small H2D copies of metadata, and stream/event ordering.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Iterable, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import ops
+from .allocator import PagePool, pages_needed
+from .decode import BatchDecodeWithPagedKVCacheWrapper
+
+__all__ = ["PagedKVCache", "SwapHandle"]
+
+
+@dataclass
+class SwapHandle:
+    """Sequences whose KV lives in pinned host memory after ``swap_out``."""
+
+    seq_ids: list[int]
+    seq_lens: list[int]
+    num_pages: list[int]
+    src_block_ids: torch.Tensor          # device int32, evicted ids (concatenated)
+    host: torch.Tensor                   # pinned uint8 [layers, n, 2, block_bytes]
+    out_event: torch.cuda.Event          # D2H complete
+    in_event: Optional[torch.cuda.Event] = None
+    dst_block_ids: Optional[torch.Tensor] = None
+    restored: bool = False
+    _keepalive: list = field(default_factory=list)
+
+    @property
+    def num_blocks(self) -> int:
+        return int(self.src_block_ids.numel())
+
+    @property
+    def bytes_per_direction(self) -> int:
+        return int(self.host.numel())
+
+
+class PagedKVCache:
+    """Per-layer paged K/V storage, block table and page pool.
+
+    Arguments follow ``MoEEngine.__init__`` (moe_engine.py:79-95, 291-301):
+    ``total_pages = kv_page_budget`` in dynamic mode, otherwise
+    ``max_seqs * ceil(max_seq_len / page_size)`` with identity block-table rows.
+    ``free_page_order`` optionally replaces the initial FIFO free list
+    ``range(total_pages)`` (e.g. a seeded permutation for a fragmented pool).
+    """
+
+    def __init__(self, num_layers: int, num_kv_heads: int, head_dim: int, max_seqs: int,
+                 max_seq_len: int, *, num_qo_heads: Optional[int] = None, page_size: int = 16,
+                 kv_page_budget: Optional[int] = None, dtype: torch.dtype = torch.bfloat16,
+                 device: str | torch.device = "cuda",
+                 free_page_order: Optional[Iterable[int]] = None,
+                 workspace_bytes: int = 128 * 1024 * 1024,
+                 staging_bytes: int = 256 * 1024 * 1024,
+                 pages_per_partition: Optional[int] = None):
+        if page_size != 16:
+            raise ValueError("page_size must be 16 (the engine's page size)")
+        self.device = torch.device(device)
+        self.num_layers = num_layers
+        self.num_kv_heads = num_kv_heads
+        self.num_heads = num_qo_heads if num_qo_heads is not None else num_kv_heads
+        self.head_dim = head_dim
+        self.page_size = page_size
+        self.dtype = dtype
+        self.max_seqs = max_seqs
+        self.max_seq_len = max_seq_len
+        self.max_pages_per_seq = math.ceil(max_seq_len / page_size)
+        self._dynamic_pages = kv_page_budget is not None
+        self.total_pages = kv_page_budget if self._dynamic_pages else max_seqs * self.max_pages_per_seq
+
+        shape = (self.total_pages, page_size, num_kv_heads, head_dim)
+        self.k_cache = [torch.zeros(shape, dtype=dtype, device=self.device) for _ in range(num_layers)]
+        self.v_cache = [torch.zeros(shape, dtype=dtype, device=self.device) for _ in range(num_layers)]
+
+        if self._dynamic_pages:
+            self.block_table = torch.full((max_seqs, self.max_pages_per_seq), -1,
+                                          dtype=torch.int32, device=self.device)
+        else:
+            self.block_table = torch.arange(max_seqs * self.max_pages_per_seq, dtype=torch.int32,
+                                            device=self.device).view(max_seqs, self.max_pages_per_seq)
+        self.seq_lens = torch.zeros(max_seqs, dtype=torch.int32, device=self.device)
+        self._seq_lens_cpu = torch.zeros(max_seqs, dtype=torch.int32)
+        self._pool = PagePool(self.total_pages, max_seqs, self.max_pages_per_seq,
+                              free_order=free_page_order) if self._dynamic_pages else None
+
+        self._workspace_bytes = workspace_bytes
+        self._ppp = pages_per_partition
+        self._decode_wrapper: Optional[BatchDecodeWithPagedKVCacheWrapper] = None
+        if self.device.type == "cuda":
+            self._init_step_buffers()
+
+        self._staging_bytes = staging_bytes
+        self._staging: Optional[torch.Tensor] = None
+        self._swap_stream: Optional[torch.cuda.Stream] = None
+        self._pending_free: list[tuple[torch.cuda.Event, list[int], list]] = []
+        self._pending_in: dict[int, torch.cuda.Event] = {}
+
+    def _init_step_buffers(self) -> None:
+        """Decode workspace + wrapper and the device page-index buffer
+        (moe_engine.py:541-575).  Only a GPU cache has them; a CPU-resident
+        instance supports the page-pool API alone.  Per-step host metadata is
+        staged through fresh pinned tensors from torch's caching host
+        allocator, which keeps each one alive until its async copy is done,
+        so planning never waits for the GPU."""
+        self._workspace_buf = torch.zeros(self._workspace_bytes, dtype=torch.uint8,
+                                          device=self.device)
+        self._decode_wrapper = BatchDecodeWithPagedKVCacheWrapper(
+            self._workspace_buf, kv_layout="NHD", use_cuda_graph=False,
+            pages_per_partition=self._ppp)
+        self._plan_indices_gpu = torch.zeros(self.max_seqs * self.max_pages_per_seq,
+                                             dtype=torch.int32, device=self.device)
+
+    def _to_device(self, arr) -> torch.Tensor:
+        """Async H2D of a small host array through a fresh pinned buffer."""
+        t = torch.as_tensor(arr)
+        return t.pin_memory().to(self.device, non_blocking=True)
+
+    def _lens_to_device(self) -> None:
+        """Refresh the device mirror of the lengths from the host copy."""
+        if self.device.type == "cuda":
+            self.seq_lens.copy_(self._seq_lens_cpu.pin_memory(), non_blocking=True)
+        else:
+            self.seq_lens.copy_(self._seq_lens_cpu)
+
+    def _require_gpu(self) -> None:
+        if self._decode_wrapper is None:
+            raise RuntimeError("this operation needs a GPU-resident PagedKVCache (device='cuda')")
+
+    # ------------------------------------------------------------ page pool
+    def _require_dynamic(self) -> None:
+        if not self._dynamic_pages:
+            raise RuntimeError("page allocation needs dynamic pages (construct with kv_page_budget)")
+
+    @property
+    def _seq_page_list(self) -> list[list[int]]:
+        self._require_dynamic()
+        return self._pool.seq_page_list
+
+    @property
+    def _free_pages(self):
+        self._require_dynamic()
+        return self._pool.free_pages
+
+    def alloc_pages(self, seq_id: int, n_pages: int) -> None:
+        """moe_engine.py:4231-4259: take n_pages from the free list (FIFO) and
+        write them to ``block_table[seq_id, current:current+n]``."""
+        self._require_dynamic()
+        if n_pages <= 0:
+            return
+        self._reclaim(need=n_pages)
+        current, pages = self._pool.alloc(seq_id, n_pages)
+        page_t = torch.tensor(pages, dtype=torch.int32)
+        if self.device.type == "cuda":
+            page_t = self._to_device(page_t)  # async: no host-GPU sync per allocation
+        self.block_table[seq_id, current:current + n_pages] = page_t
+
+    def free_seq_pages(self, seq_id: int) -> None:
+        """moe_engine.py:4261-4273: pages back to the free list, row -> -1."""
+        self._require_dynamic()
+        pages = self._pool.release(seq_id)
+        if pages:
+            self.block_table[seq_id, :len(pages)] = -1
+
+    def ensure_pages(self, seq_id: int, needed_pages: int) -> None:
+        """moe_engine.py:4275-4283: grow seq_id to needed_pages (no-op if enough)."""
+        self._require_dynamic()
+        current = self._pool.seq_pages(seq_id)
+        if needed_pages > current:
+            self.alloc_pages(seq_id, needed_pages - current)
+
+    @property
+    def pages_free(self) -> int:
+        self._require_dynamic()
+        return self._pool.pages_free
+
+    @property
+    def pages_in_use(self) -> int:
+        self._require_dynamic()
+        return self._pool.pages_in_use
+
+    def seq_pages(self, seq_id: int) -> int:
+        if not self._dynamic_pages:
+            return self.max_pages_per_seq
+        return self._pool.seq_pages(seq_id)
+
+    def free_seq(self, seq_id: int) -> None:
+        """moe_engine.py:4212-4227: seq_len -> 0 and (dynamic) pages freed."""
+        self._seq_lens_cpu[seq_id] = 0
+        self.seq_lens[seq_id] = 0
+        self._pending_in.pop(seq_id, None)
+        if self._dynamic_pages:
+            self.free_seq_pages(seq_id)
+
+    def reset(self) -> None:
+        """moe_engine.py:4185-4210: zero lengths and caches, refill the pool."""
+        self.synchronize_swaps()
+        self.seq_lens.zero_()
+        self._seq_lens_cpu.zero_()
+        for kc, vc in zip(self.k_cache, self.v_cache):
+            kc.zero_()
+            vc.zero_()
+        if self._dynamic_pages:
+            self._pool.reset()
+            self.block_table.fill_(-1)
+        self._pending_free.clear()
+        self._pending_in.clear()
+
+    # ----------------------------------------------------- snapshot / fill
+    def fill_kv_random(self, std: float = 0.01, generator: Optional[torch.Generator] = None) -> None:
+        for kc, vc in zip(self.k_cache, self.v_cache):
+            kc.normal_(0, std, generator=generator)
+            vc.normal_(0, std, generator=generator)
+
+    def kv_snapshot(self):
+        return ([kc.clone() for kc in self.k_cache], [vc.clone() for vc in self.v_cache])
+
+    def kv_restore(self, snapshot) -> None:
+        a, b = snapshot
+        for kc, s in zip(self.k_cache, a):
+            kc.copy_(s)
+        for vc, s in zip(self.v_cache, b):
+            vc.copy_(s)
+
+    # --------------------------------------------------------- step metadata
+    def _sync_seqs(self, seq_ids: Sequence[int]) -> None:
+        """Order the current stream after pending swap-ins of these sequences."""
+        if not self._pending_in:
+            return
+        cur = torch.cuda.current_stream(self.device)
+        for sid in seq_ids:
+            ev = self._pending_in.pop(int(sid), None)
+            if ev is not None:
+                cur.wait_event(ev)
+
+    def slot_mapping(self, seq_ids: Sequence[int], num_new_tokens: Sequence[int],
+                     graph_n: Optional[int] = None) -> torch.Tensor:
+        """Slots of the next tokens of each sequence (positions continue from
+        ``seq_lens``), padded with -1 to ``graph_n`` tokens, computed on the
+        device (moe_engine.py:3475-3541).  Does not advance ``seq_lens``."""
+        self._require_gpu()
+        r = len(seq_ids)
+        n = int(sum(num_new_tokens))
+        graph_n = n if graph_n is None else graph_n
+        out = torch.empty(graph_n, dtype=torch.int64, device=self.device)
+        if r == 0 or graph_n == 0:
+            out.fill_(-1)
+            return out
+        ids = self._to_device(np.asarray(seq_ids, dtype=np.int32))
+        qsl = np.zeros(r + 1, dtype=np.int32)
+        np.cumsum(np.asarray(num_new_tokens, dtype=np.int32), out=qsl[1:])
+        qsl_d = self._to_device(qsl)
+        # Safety sync of the device lengths from the host mirror (the engine
+        # does the same at moe_engine.py:3511).
+        self._lens_to_device()
+        ops.compute_slot_mapping(self.block_table, ids, qsl_d, self.seq_lens, n, out,
+                                 block_size=self.page_size)
+        return out
+
+    def advance(self, seq_ids: Sequence[int], num_new_tokens: Sequence[int] | int = 1) -> None:
+        """``_seq_lens_cpu[sid] += n`` (and the device mirror)."""
+        if isinstance(num_new_tokens, int):
+            num_new_tokens = [num_new_tokens] * len(seq_ids)
+        for sid, n in zip(seq_ids, num_new_tokens):
+            self._seq_lens_cpu[sid] += int(n)
+        self._lens_to_device()
+
+    def plan_decode(self, seq_ids: Sequence[int]) -> None:
+        """moe_engine.py:1896-1955: indptr / last_page_len on the host,
+        page indices flattened on the device, then ``wrapper.plan``."""
+        self._require_gpu()
+        b = len(seq_ids)
+        if b == 0:
+            return
+        self._sync_seqs(seq_ids)
+        ids = np.asarray(seq_ids, dtype=np.int64)
+        lens = self._seq_lens_cpu.numpy()[ids].astype(np.int32)
+        nblk = (lens + self.page_size - 1) // self.page_size
+        indptr = np.zeros(b + 1, dtype=np.int32)
+        np.cumsum(nblk, out=indptr[1:])
+        lpl = lens % self.page_size
+        lpl = np.where((lpl == 0) & (lens != 0), self.page_size, lpl).astype(np.int32)
+        indptr_d = self._to_device(indptr)
+        ids_d = self._to_device(ids.astype(np.int32))
+        ops.copy_page_indices(self.block_table, indptr_d, self._plan_indices_gpu, seq_ids=ids_d)
+        total = int(indptr[b])
+        self._decode_wrapper.plan(
+            torch.from_numpy(indptr), self._plan_indices_gpu[:total], torch.from_numpy(lpl),
+            num_qo_heads=self.num_heads, num_kv_heads=self.num_kv_heads, head_dim=self.head_dim,
+            page_size=self.page_size, pos_encoding_mode="NONE", q_data_type=self.dtype)
+
+    def prepare_decode_step(self, seq_ids: Sequence[int], graph_n: Optional[int] = None) -> torch.Tensor:
+        """Setup of a pure-decode step in the engine's order
+        (moe_engine.py:2655-2695, 3511-3556): slot mapping from the current
+        lengths, then ``seq_lens += 1``, then plan.  Pages must already cover
+        the new token (the scheduler's ``ensure_pages``)."""
+        self._require_gpu()
+        self._sync_seqs(seq_ids)
+        slots = self.slot_mapping(seq_ids, [1] * len(seq_ids), graph_n)
+        for sid in seq_ids:
+            self._seq_lens_cpu[sid] += 1
+        self._lens_to_device()
+        self.plan_decode(seq_ids)
+        return slots
+
+    # ------------------------------------------------------- per-layer ops
+    def append(self, layer: int, key: torch.Tensor, value: torch.Tensor,
+               slot_mapping: torch.Tensor) -> None:
+        ops.reshape_and_cache_flash(key, value, self.k_cache[layer], self.v_cache[layer],
+                                    slot_mapping, "auto")
+
+    def decode(self, layer: int, q: torch.Tensor, out: Optional[torch.Tensor] = None,
+               return_lse: bool = False):
+        self._require_gpu()
+        return self._decode_wrapper.run(q, (self.k_cache[layer], self.v_cache[layer]),
+                                        out=out, return_lse=return_lse)
+
+    def gather(self, layer: int, seq_ids: Sequence[int], out_key: Optional[torch.Tensor] = None,
+               out_value: Optional[torch.Tensor] = None):
+        """Contiguous ``[sum(len), heads, dim]`` K and V of the given sequences
+        (their current ``seq_lens``), in order."""
+        self._require_gpu()
+        self._sync_seqs(seq_ids)
+        ids = np.asarray(seq_ids, dtype=np.int64)
+        lens = self._seq_lens_cpu.numpy()[ids].astype(np.int32)
+        cu = np.zeros(len(ids) + 1, dtype=np.int32)
+        np.cumsum(lens, out=cu[1:])
+        cu_t = self._to_device(cu)
+        rows = self.block_table.index_select(0, self._to_device(ids))
+        total = int(cu[-1])
+        if out_key is None:
+            out_key = torch.empty(total, self.num_kv_heads, self.head_dim, dtype=self.dtype,
+                                  device=self.device)
+        if out_value is None:
+            out_value = torch.empty_like(out_key)
+        return ops.gather_kv(self.k_cache[layer], self.v_cache[layer], rows, cu_t,
+                             int(lens.max()) if len(lens) else 0, out_key, out_value)
+
+    # ----------------------------------------------------------------- swap
+    def _side_stream(self) -> torch.cuda.Stream:
+        if self._swap_stream is None:
+            self._swap_stream = torch.cuda.Stream(device=self.device)
+        return self._swap_stream
+
+    def _staging_buf(self) -> torch.Tensor:
+        if self._staging is None:
+            self._staging = torch.empty(self._staging_bytes, dtype=torch.uint8, device=self.device)
+        return self._staging
+
+    def _reclaim(self, need: int = 0) -> None:
+        """Return pages of finished swap-outs to the free list; block on the
+        oldest pending swap-out only if the pool cannot serve ``need`` pages."""
+        still = []
+        for ev, pages, keep in self._pending_free:
+            if ev.query():
+                self._pool.give_back(pages)
+            else:
+                still.append((ev, pages, keep))
+        self._pending_free = still
+        while self._pending_free and self._pool.pages_free < need:
+            ev, pages, keep = self._pending_free.pop(0)
+            ev.synchronize()
+            self._pool.give_back(pages)
+
+    def synchronize_swaps(self) -> None:
+        if self._swap_stream is not None:
+            self._swap_stream.synchronize()
+        if self._dynamic_pages:
+            self._reclaim(need=self.total_pages + 1)
+
+    def swap_out(self, seq_ids: Sequence[int]) -> SwapHandle:
+        """Evict whole sequences to pinned host memory on the side stream.
+
+        The sequences stop being resident (pages detached, block-table rows
+        -1, length 0); their pages rejoin the free list once the copy is done.
+        The side stream first waits for all work already enqueued on the
+        current stream, so earlier appends are included."""
+        self._require_gpu()
+        self._require_dynamic()
+        seq_ids = [int(s) for s in seq_ids]
+        cur = torch.cuda.current_stream(self.device)
+        self._sync_seqs(seq_ids)
+        lens, npages, ids = [], [], []
+        for sid in seq_ids:
+            pages = self._pool.detach(sid)
+            lens.append(int(self._seq_lens_cpu[sid]))
+            npages.append(len(pages))
+            ids.extend(pages)
+            if pages:
+                self.block_table[sid, :len(pages)] = -1
+            self._seq_lens_cpu[sid] = 0
+        self._lens_to_device()
+        n = len(ids)
+        bb = ops.block_bytes(self.k_cache[0])
+        host = torch.empty(self.num_layers * n * 2 * bb, dtype=torch.uint8, pin_memory=True)
+        ids_t = self._to_device(np.asarray(ids, dtype=np.int32))
+        side = self._side_stream()
+        side.wait_stream(cur)
+        staging = self._staging_buf()
+        ops.swap_out_blocks(self.k_cache, self.v_cache, ids_t, host, staging, stream=side)
+        ids_t.record_stream(side)
+        ev = torch.cuda.Event()
+        ev.record(side)
+        # The host buffer must outlive the D2H copy even if the handle is dropped.
+        self._pending_free.append((ev, ids, [ids_t, host]))
+        return SwapHandle(seq_ids, lens, npages, ids_t, host, ev)
+
+    def swap_in(self, handle: SwapHandle, wait: bool = False) -> None:
+        """Restore an evicted handle into freshly allocated pages.
+
+        Allocation and block-table updates happen now; the H2D copies and the
+        scatter run on the side stream after everything already enqueued on
+        the current stream.  Later ``plan_decode`` / ``gather`` / ``swap_out``
+        of these sequences make the current stream wait for the restore;
+        ``wait=True`` does so immediately."""
+        self._require_gpu()
+        self._require_dynamic()
+        if handle.restored:
+            raise RuntimeError("swap handle already restored")
+        cur = torch.cuda.current_stream(self.device)
+        dst = []
+        for sid, n, ln in zip(handle.seq_ids, handle.num_pages, handle.seq_lens):
+            if self._pool.seq_pages(sid) != 0 or int(self._seq_lens_cpu[sid]) != 0:
+                raise RuntimeError(f"seq {sid} is resident; free it before swap_in")
+            self.alloc_pages(sid, n)
+            dst.extend(self._pool.seq_page_list[sid])
+            self._seq_lens_cpu[sid] = ln
+        self._lens_to_device()
+        dst_t = self._to_device(np.asarray(dst, dtype=np.int32))
+        side = self._side_stream()
+        side.wait_stream(cur)
+        side.wait_event(handle.out_event)
+        ops.swap_in_blocks(handle.host, dst_t, self.k_cache, self.v_cache, self._staging_buf(),
+                           stream=side)
+        dst_t.record_stream(side)
+        ev = torch.cuda.Event()
+        ev.record(side)
+        self._pending_free.append((ev, [], [dst_t, handle.host]))
+        handle.in_event = ev
+        handle.dst_block_ids = dst_t
+        handle.restored = True
+        for sid in handle.seq_ids:
+            self._pending_in[sid] = ev
+        if wait:
+            self._sync_seqs(handle.seq_ids)

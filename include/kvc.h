@@ -1,0 +1,236 @@
+/*
+ * kvc.h — C ABI of the MI355X (gfx950) paged KV-cache library, libkvc.so.
+ *
+ * Every entry point takes plain device/host pointers, sizes and strides and an
+ * explicit hipStream_t (passed as void*), returns an int status (KVC_OK == 0),
+ * and never allocates device memory: buffers (caches, tables, workspace,
+ * staging, pinned host memory) are owned by the caller.  A failed call leaves
+ * a human-readable reason in kvc_last_error() (thread-local).
+ *
+ * Cache layout ("NHD", one tensor per layer for K and one for V):
+ *     cache[num_blocks][block_size][num_kv_heads][head_dim]
+ * with an arbitrary block stride (so a [num_blocks, 2, block_size, H, D]
+ * combined tensor can be passed as two views) and a token stride inside a
+ * block.  The heads of one token must be contiguous (head stride == head_dim).
+ * A slot is   block_id * block_size + offset_in_block.
+ *
+ * Reference interfaces (file:line in aojsd/GPU_Offloading) each entry point
+ * replaces are cited beside it.  Strides are in ELEMENTS unless the name ends
+ * in _bytes.
+ */
+#ifndef KVC_H_
+#define KVC_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum kvc_status {
+  KVC_OK = 0,
+  KVC_ERR_INVALID_ARG = 1,   /* null pointer, negative size, bad stride   */
+  KVC_ERR_UNSUPPORTED = 2,   /* shape/dtype combination not compiled      */
+  KVC_ERR_ALIGNMENT = 3,     /* pointer or stride breaks vector alignment */
+  KVC_ERR_WORKSPACE = 4,     /* workspace / staging buffer too small      */
+  KVC_ERR_HIP = 5            /* a HIP runtime call or launch failed       */
+};
+
+/* Library version (major*10000 + minor*100 + patch). */
+int kvc_version(void);
+/* Static description of a status code. */
+const char* kvc_status_string(int status);
+/* Detail of the last failed call on this thread ("" if none). */
+const char* kvc_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * (a5) KV append — slot_mapping scatter.
+ * Replaces vLLM _C reshape_and_cache_flash as called at
+ *   src/MoE/moe_engine.py:2059-2062 and :2344-2347
+ *   (PyTorch twin with identical semantics: moe_engine.py:2196-2198).
+ * For every token i < num_tokens with 0 <= slot_mapping[i] < num_blocks*block_size:
+ *   key_cache[slot/bs][slot%bs][:][:]   = key[i][:][:]
+ *   value_cache[slot/bs][slot%bs][:][:] = value[i][:][:]
+ * A negative slot is padding and is skipped (moe_engine.py:3539-3540); an
+ * out-of-range slot is also skipped and counted in *oob_count when that
+ * device pointer is non-null (the count is accumulated, not reset).
+ * Pure byte copy: elem_bytes is the element size (2 for bf16/fp16).
+ * ---------------------------------------------------------------------- */
+int kvc_reshape_and_cache_flash(
+    const void* key, const void* value,
+    void* key_cache, void* value_cache,
+    const int64_t* slot_mapping,
+    int64_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+    int32_t block_size, int64_t num_blocks, int32_t elem_bytes,
+    int64_t key_token_stride, int64_t value_token_stride,
+    int64_t cache_block_stride, int64_t cache_token_stride,
+    int32_t* oob_count, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Block-table gather into contiguous [tokens, num_kv_heads, head_dim].
+ * New API (the reference engine has no gather; its closed form is
+ * cache[bt[seq, :nb]].flatten(0,1)[:len], cf. the un-permute in
+ * src/dense/scratch_examples/vllm_paged_attn.py:161-190).
+ * Sequence b contributes tokens [seq_starts[b], seq_starts[b] + len_b) of its
+ * logical KV (len_b = cu_seq_lens[b+1] - cu_seq_lens[b]) to output rows
+ * [cu_seq_lens[b], cu_seq_lens[b+1]).  seq_starts may be null (all zero).
+ * max_seq_len bounds every len_b (host-side value, sizes the grid; rows past
+ * it are not written).  block_table_width is the number of entries per
+ * block-table row.  Rows whose position falls outside the row or whose entry is
+ * outside [0, num_blocks) are zero-filled and counted in *oob_count when
+ * non-null.
+ * ---------------------------------------------------------------------- */
+int kvc_gather_kv(
+    const void* key_cache, const void* value_cache,
+    const int32_t* block_table, int64_t block_table_row_stride,
+    int32_t block_table_width,
+    const int32_t* cu_seq_lens, const int32_t* seq_starts,
+    int32_t batch, int32_t max_seq_len,
+    int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+    int64_t num_blocks, int32_t elem_bytes,
+    int64_t cache_block_stride, int64_t cache_token_stride,
+    void* out_key, void* out_value, int64_t out_token_stride,
+    int32_t* oob_count, void* stream);
+
+/* ------------------------------------------------------------------------
+ * (a6/a7/a8) Paged GQA decode attention (bf16 in/out, fp32 accumulate).
+ * Replaces FlashInfer BatchDecodeWithPagedKVCacheWrapper.plan/run as called at
+ *   src/MoE/moe_engine.py:1352-1358, :1949-1955 (plan) and :3907-3909 (run).
+ * Request b attends over the pages indices[indptr[b] .. indptr[b+1]) where
+ * the final page holds last_page_len[b] tokens (1..page_size):
+ *   out[b][hq] = softmax_t(sm_scale * q[b][hq] . K[t][hq/group]) . V[t][hq/group]
+ * group = num_qo_heads / num_kv_heads.  Optional lse[b][hq] receives the
+ * natural-log log-sum-exp of the scaled logits (-inf for an empty request).
+ * The context is split into partitions of pages_per_partition pages; partial
+ * results go to the workspace and are merged with the log-sum-exp rule of
+ * src/dense/offload_kv_attn.py:24-39.
+ *
+ * kvc_decode_plan is host-only (no device access): it picks the partition size
+ * from the host copy of indptr, like FlashInfer plan() which also reads a host
+ * indptr.  pages_per_partition_hint > 0 forces the size (rounded up to a
+ * multiple of 4).  kvc_decode_workspace_bytes sizes the workspace.
+ * ---------------------------------------------------------------------- */
+typedef struct kvc_decode_schedule {
+  int32_t batch;
+  int32_t num_qo_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t page_size;
+  int32_t pages_per_partition;
+  int32_t max_partitions;     /* max over requests of ceil(pages/ppp) */
+  int32_t total_pages;        /* indptr[batch]                         */
+  int32_t num_empty;          /* requests with no pages (output zero)  */
+  int64_t workspace_bytes;    /* bytes kvc_batch_decode_run will use   */
+} kvc_decode_schedule;
+
+int kvc_decode_plan(const int32_t* indptr_host, int32_t batch,
+                    int32_t num_qo_heads, int32_t num_kv_heads,
+                    int32_t head_dim, int32_t page_size,
+                    int32_t pages_per_partition_hint, int32_t num_cus,
+                    kvc_decode_schedule* schedule);
+
+int64_t kvc_decode_workspace_bytes(int32_t batch, int32_t num_qo_heads,
+                                   int32_t head_dim, int32_t max_partitions);
+
+int kvc_batch_decode_run(
+    const kvc_decode_schedule* schedule,
+    const void* q, int64_t q_batch_stride,
+    const void* key_cache, const void* value_cache,
+    int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t num_blocks,
+    const int32_t* indptr, const int32_t* indices, int64_t num_indices,
+    const int32_t* last_page_len,
+    float sm_scale,
+    void* workspace, int64_t workspace_bytes,
+    void* out, int64_t out_batch_stride, float* lse, void* stream);
+
+/* ------------------------------------------------------------------------
+ * (a8) Merge two attention states, fp32 math:
+ *   lse = logaddexp(lse1, lse2); out = out1*e^(lse1-lse) + out2*e^(lse2-lse)
+ * Restates src/dense/offload_kv_attn.py:24-39 on the device.  out* are bf16
+ * [n, head_dim] rows, lse* fp32 [n] natural log.  out may alias out1 or out2;
+ * lse (nullable) must not alias lse1 or lse2.
+ * ---------------------------------------------------------------------- */
+int kvc_merge_attention_states(const void* out1, const float* lse1,
+                               const void* out2, const float* lse2,
+                               int64_t n, int32_t head_dim,
+                               void* out, float* lse, void* stream);
+
+/* ------------------------------------------------------------------------
+ * (a10) KV block eviction / restore.  New API; precedents are
+ * kv_snapshot/kv_restore (src/MoE/moe_engine.py:4163-4183) and the pinned
+ * H2D/D2H side-stream pipeline (src/dense/include/paged_offload_transformer.py:
+ * 111-134, 394-418).
+ * staging layout: [n][2][block_bytes]  (K block then V block), where
+ * block_bytes = block_size * num_kv_heads * head_dim * elem_bytes and a block
+ * occupies block_bytes contiguous bytes at cache + id * cache_block_stride_bytes.
+ * Ids outside [0, num_blocks) are skipped and counted in *oob_count.
+ * ---------------------------------------------------------------------- */
+int kvc_gather_blocks(const void* key_cache, const void* value_cache,
+                      int64_t cache_block_stride_bytes, int64_t block_bytes,
+                      int64_t num_blocks, const int32_t* block_ids,
+                      int64_t n, void* staging, int32_t* oob_count,
+                      void* stream);
+
+int kvc_scatter_blocks(const void* staging, const int32_t* block_ids,
+                       int64_t n, void* key_cache, void* value_cache,
+                       int64_t cache_block_stride_bytes, int64_t block_bytes,
+                       int64_t num_blocks, int32_t* oob_count, void* stream);
+
+/* Swap out: gather the n blocks to the device staging buffer then
+ * hipMemcpyAsync them to host_dst ([n][2][block_bytes], pinned host memory),
+ * in chunks of at most staging_bytes, all on `stream`.  Swap in is the
+ * reverse (H2D into staging, then scatter into dst block ids).  Both return as
+ * soon as the work is enqueued. */
+int kvc_swap_out(const void* key_cache, const void* value_cache,
+                 int64_t cache_block_stride_bytes, int64_t block_bytes,
+                 int64_t num_blocks, const int32_t* block_ids, int64_t n,
+                 void* staging, int64_t staging_bytes, void* host_dst,
+                 int32_t* oob_count, void* stream);
+
+int kvc_swap_in(const void* host_src, const int32_t* block_ids, int64_t n,
+                void* key_cache, void* value_cache,
+                int64_t cache_block_stride_bytes, int64_t block_bytes,
+                int64_t num_blocks, void* staging, int64_t staging_bytes,
+                int32_t* oob_count, void* stream);
+
+/* ------------------------------------------------------------------------
+ * (f1) Step-setup metadata on the device.
+ * kvc_compute_slot_mapping replaces vLLM prepare_pos_seq_lens +
+ * _compute_slot_mappings_kernel as called at src/MoE/moe_engine.py:3514-3541
+ * (eager twins :1308-1316, :2677-2695).  Request r (seq id seq_ids[r]) owns
+ * tokens [query_start_loc[r], query_start_loc[r+1]); token i of it sits at
+ * position num_computed[seq_ids[r]] + (i - query_start_loc[r]) and its slot is
+ *   block_table[seq, pos / block_size] * block_size + pos % block_size.
+ * An unallocated entry (-1) yields a negative slot, which the append skips,
+ * exactly as the reference formula does.  Token slots [num_tokens,
+ * num_tokens_padded) are set to -1 (PAD) and their positions to 0; tokens whose
+ * seq id is outside [0, block_table_rows) or whose page is outside the row
+ * also get slot -1.  positions may be null.
+ *
+ * kvc_copy_page_indices replaces _copy_page_indices_kernel + the row
+ * index_select at moe_engine.py:1937-1946: for request r (block-table row
+ * seq_ids[r], or r when seq_ids is null)
+ *   indices[indptr[r] + j] = block_table[row][j],  j < indptr[r+1]-indptr[r].
+ * ---------------------------------------------------------------------- */
+int kvc_compute_slot_mapping(
+    const int32_t* block_table, int64_t block_table_row_stride,
+    int32_t block_table_rows, int32_t max_pages_per_seq,
+    const int32_t* seq_ids, const int32_t* query_start_loc,
+    const int32_t* num_computed, int32_t num_reqs,
+    int32_t num_tokens, int32_t num_tokens_padded, int32_t block_size,
+    int64_t* slot_mapping, int32_t* positions, void* stream);
+
+int kvc_copy_page_indices(const int32_t* block_table,
+                          int64_t block_table_row_stride,
+                          int32_t block_table_rows,
+                          const int32_t* seq_ids, const int32_t* indptr,
+                          int32_t num_reqs, int32_t max_pages_per_req,
+                          int32_t* indices, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVC_H_ */

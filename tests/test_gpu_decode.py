@@ -1,0 +1,220 @@
+"""GPU parity of paged GQA decode attention: against the fp32 CPU oracle and
+an fp32 torch SDPA reference, max-abs-error <= 2e-2 and mean-abs-error <= 2e-3
+on the bf16 output."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_offloading_amd import ops, workloads
+from gpu_offloading_amd.decode import BatchDecodeWithPagedKVCacheWrapper
+from helpers import assert_attn_close, randn_bf16, u16
+from oracle import kv_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+WS = 128 * 1024 * 1024
+
+
+def _paged(lens, hkv, d, seed, total_pages=None, device=None, fill_std=1.0):
+    """Random paged cache holding sequences of the given lengths in blocks of a
+    seeded permuted pool; returns (kc, vc, block_table, indptr, indices, lpl)."""
+    need = sum((ln + 15) // 16 for ln in lens)
+    total = total_pages or need + 8
+    pool = orc.FifoPagePool(total, len(lens), max(1, max((ln + 15) // 16 for ln in lens)),
+                            free_order=workloads.randperm(total, seed))
+    for s, ln in enumerate(lens):
+        pool.ensure_pages(s, (ln + 15) // 16)
+    kc = (torch.randn(total, 16, hkv, d, device=device) * fill_std).to(torch.bfloat16)
+    vc = torch.randn(total, 16, hkv, d, device=device).to(torch.bfloat16)
+    indptr, lpl = orc.plan_decode(lens)
+    indices = orc.page_indices(pool.block_table, range(len(lens)), indptr)
+    return kc, vc, pool.block_table, indptr, indices, lpl
+
+
+def _run(gpu, q, kc, vc, indptr, indices, lpl, hq, hkv, d, ppp=None, return_lse=True):
+    w = BatchDecodeWithPagedKVCacheWrapper(torch.empty(WS, dtype=torch.uint8, device=gpu),
+                                           pages_per_partition=ppp)
+    w.plan(torch.from_numpy(indptr), torch.from_numpy(indices).to(gpu), torch.from_numpy(lpl),
+           num_qo_heads=hq, num_kv_heads=hkv, head_dim=d, page_size=16)
+    res = w.run(q, (kc, vc), return_lse=return_lse)
+    torch.cuda.synchronize()
+    return res, w
+
+
+def _sdpa_ref(q, kc, vc, bt, lens):
+    """fp32 torch SDPA (enable_gqa) on the contiguous K/V of each sequence,
+    reached through the block table with torch indexing (independent of the
+    oracle and of the kernel)."""
+    qf = q.float().cpu()
+    kc, vc = kc.float().cpu(), vc.float().cpu()
+    outs = []
+    for b, ln in enumerate(lens):
+        pages = torch.from_numpy(bt[b, :(ln + 15) // 16].astype(np.int64))
+        K = kc[pages].flatten(0, 1)[:ln].transpose(0, 1).contiguous()  # [Hkv, n, D]
+        V = vc[pages].flatten(0, 1)[:ln].transpose(0, 1).contiguous()
+        o = torch.nn.functional.scaled_dot_product_attention(
+            qf[b][:, None, :], K, V, enable_gqa=True)                      # [Hq, 1, D]
+        outs.append(o[:, 0])
+    return torch.stack(outs).numpy()
+
+
+def test_decode_cfg1_vs_oracle_and_sdpa(gpu):
+    cfg = workloads.config1(seed=0)
+    sh = cfg.shape
+    lens = [ln + 1 for ln in cfg.seq_lens]  # the step's own token is attended
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, sh.num_kv_heads, sh.head_dim, 1,
+                                              total_pages=cfg.total_pages)
+    for layer in range(sh.num_layers):
+        q = randn_bf16((len(lens), sh.num_qo_heads, sh.head_dim), 50 + layer)
+        (out, lse), _ = _run(gpu, q.to(gpu), kc.to(gpu), vc.to(gpu), indptr, indices, lpl,
+                             sh.num_qo_heads, sh.num_kv_heads, sh.head_dim)
+        ref, ref_lse = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
+        assert_attn_close(out.float().cpu().numpy(), ref)
+        assert_attn_close(out.float().cpu().numpy(), _sdpa_ref(q, kc, vc, bt, lens))
+        assert np.allclose(lse.cpu().numpy(), ref_lse, atol=1e-3, rtol=1e-4)
+
+
+def test_decode_one_token_context_returns_v0_exactly(gpu):
+    lens = [1, 1, 17, 16]  # 17: one token in the second page; 16: full page
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, 8, 128, 2)
+    q = randn_bf16((4, 32, 128), 3, device=gpu)
+    (out, lse), _ = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, 32, 8, 128)
+    for b in (0, 1):
+        v0 = vc[bt[b, 0], 0]                                   # [Hkv, D]
+        assert torch.equal(out[b].cpu(), v0.repeat_interleave(4, dim=0))
+    ref, _ = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
+    assert_attn_close(out.float().cpu().numpy(), ref)
+
+
+def test_decode_ignores_nan_in_slots_past_the_end(gpu):
+    lens = [5, 33]
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, 8, 128, 4)
+    # poison every slot past each sequence's end with NaN bit patterns
+    for b, ln in enumerate(lens):
+        last = bt[b, (ln - 1) // 16]
+        kc[last, ln % 16 or 16:] = float("nan")
+        vc[last, ln % 16 or 16:] = float("nan")
+    q = randn_bf16((2, 32, 128), 5, device=gpu)
+    (out, _), _ = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, 32, 8, 128)
+    ref, _ = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
+    assert_attn_close(out.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("ppp", [4, 8, 12, 64, None])
+def test_decode_partition_sizes_agree(gpu, ppp):
+    lens = [1, 15, 16, 17, 64, 100, 511, 512, 513, 2000]
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, 8, 128, 6)
+    q = randn_bf16((len(lens), 32, 128), 7, device=gpu)
+    (out, lse), w = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, 32, 8, 128, ppp=ppp)
+    if ppp is not None:
+        assert w.schedule.pages_per_partition == (ppp + 3) // 4 * 4
+    ref, ref_lse = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
+    assert_attn_close(out.float().cpu().numpy(), ref)
+    assert np.allclose(lse.cpu().numpy(), ref_lse, atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("group,d", [(1, 128), (2, 128), (8, 128), (4, 64), (1, 256), (4, 256), (8, 64)])
+def test_decode_group_sizes_and_head_dims(gpu, group, d):
+    hkv = 4
+    hq = hkv * group
+    lens = [3, 77, 300, 1025]
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, hkv, d, 8)
+    q = randn_bf16((len(lens), hq, d), 9, device=gpu)
+    (out, _), _ = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, hq, hkv, d, ppp=8)
+    ref, _ = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
+    assert_attn_close(out.float().cpu().numpy(), ref)
+
+
+def test_decode_empty_request_gives_zero_and_neg_inf_lse(gpu):
+    lens = [0, 40, 0]
+    kc, vc, bt, indptr, indices, lpl = _paged([40], 8, 128, 10)
+    indptr = np.array([0, 0, 3, 3], np.int32)
+    lpl = np.array([0, 8, 0], np.int32)
+    q = randn_bf16((3, 32, 128), 11, device=gpu)
+    for ppp in (None, 4):
+        (out, lse), _ = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, 32, 8, 128, ppp=ppp)
+        assert int(out[0].abs().sum()) == 0 and int(out[2].abs().sum()) == 0
+        assert torch.isneginf(lse[0]).all() and torch.isneginf(lse[2]).all()
+        ref, _ = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
+        assert_attn_close(out.float().cpu().numpy(), ref)
+
+
+def test_decode_q_view_and_out_buffer(gpu):
+    # q as q_buf[:B] of a larger static buffer, out written into a view of a
+    # larger [N, Hq*D] buffer (the engine's attn_out_buf), combined KV tensor.
+    lens = [40, 200, 1000]
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, 8, 128, 12)
+    q_buf = randn_bf16((8, 32, 128), 13, device=gpu)
+    kv = torch.stack([kc, vc], dim=1).to(gpu)  # [P, 2, 16, H, D]
+    w = BatchDecodeWithPagedKVCacheWrapper(torch.empty(WS, dtype=torch.uint8, device=gpu))
+    w.plan(torch.from_numpy(indptr), torch.from_numpy(indices), torch.from_numpy(lpl), 32, 8, 128, 16)
+    out_buf = torch.zeros(8, 32 * 128, dtype=torch.bfloat16, device=gpu)
+    out = w.run(q_buf[:3], kv, out=out_buf[:3].view(3, 32, 128))
+    torch.cuda.synchronize()
+    assert out.data_ptr() == out_buf.data_ptr()
+    ref, _ = orc.paged_decode(u16(q_buf[:3]), u16(kc), u16(vc), indptr, indices, lpl)
+    assert_attn_close(out_buf[:3].view(3, 32, 128).float().cpu().numpy(), ref)
+    assert int(out_buf[3:].abs().sum()) == 0
+
+
+def test_decode_cfg2_one_layer(gpu):
+    """Config 2 shapes (B=64, ctx U[512, 4096] + the step's token), one layer."""
+    cfg = workloads.config2(seed=0)
+    lens = [ln + 1 for ln in cfg.seq_lens]
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, 8, 128, 14, device=gpu)
+    q = randn_bf16((64, 32, 128), 15, device=gpu)
+    (out, lse), w = _run(gpu, q, kc, vc, indptr, indices, lpl, 32, 8, 128)
+    assert w.schedule.max_partitions > 1  # exercises the split-K merge
+    ref, ref_lse = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
+    assert_attn_close(out.float().cpu().numpy(), ref)
+    assert np.allclose(lse.cpu().numpy(), ref_lse, atol=2e-3, rtol=1e-4)
+
+
+def test_decode_cfg4_long_context(gpu):
+    """Config 4: 16 x 32768 tokens, logits std ~3 (q scaled by 3).  Four of
+    the requests (first, last and two inside) are checked against the oracle."""
+    cfg = workloads.config4(seed=0)
+    lens = cfg.seq_lens
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, 8, 128, 16, device=gpu)
+    q = randn_bf16((16, 32, 128), 17, std=3.0, device=gpu)
+    (out, lse), _ = _run(gpu, q, kc, vc, indptr, indices, lpl, 32, 8, 128)
+    kcn, vcn = u16(kc), u16(vc)
+    got = out.float().cpu().numpy()
+    for b in (0, 5, 10, 15):
+        sl = slice(b, b + 1)
+        ip = indptr[sl.start:sl.stop + 1] - indptr[b]
+        idx = indices[indptr[b]:indptr[b + 1]]
+        ref, _ = orc.paged_decode(u16(q[sl]), kcn, vcn, ip, idx, lpl[sl])
+        assert_attn_close(got[sl], ref)
+
+
+def test_merge_attention_states_matches_oracle(gpu):
+    o1 = randn_bf16((5, 32, 128), 20, device=gpu)
+    o2 = randn_bf16((5, 32, 128), 21, device=gpu)
+    l1 = torch.randn(5, 32, device=gpu) * 4
+    l2 = torch.randn(5, 32, device=gpu) * 4
+    l2[0, 0] = float("-inf")
+    out, lse = ops.merge_attention_states(o1, l1, o2, l2)
+    ref_o, ref_l = orc.merge_attention_states(o1.float().cpu().numpy(), l1.cpu().numpy(),
+                                              o2.float().cpu().numpy(), l2.cpu().numpy())
+    assert_attn_close(out.float().cpu().numpy(), ref_o)
+    assert np.allclose(lse.cpu().numpy(), ref_l, atol=1e-5, rtol=1e-5)
+
+
+def test_decode_split_merge_equals_whole(gpu):
+    """Attention over a context split in two halves, merged with
+    merge_attention_states, equals attention over the whole context."""
+    lens = [700]
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, 8, 128, 22)
+    q = randn_bf16((1, 32, 128), 23, device=gpu)
+    kcg, vcg = kc.to(gpu), vc.to(gpu)
+    (whole, _), _ = _run(gpu, q, kcg, vcg, indptr, indices, lpl, 32, 8, 128)
+    a_idx, b_idx = indices[:20], indices[20:]
+    (o1, l1), _ = _run(gpu, q, kcg, vcg, np.array([0, 20], np.int32), a_idx,
+                       np.array([16], np.int32), 32, 8, 128)
+    (o2, l2), _ = _run(gpu, q, kcg, vcg, np.array([0, len(b_idx)], np.int32), b_idx,
+                       lpl, 32, 8, 128)
+    merged, _ = ops.merge_attention_states(o1, l1, o2, l2)
+    assert_attn_close(merged.float().cpu().numpy(), whole.float().cpu().numpy())

@@ -1,0 +1,129 @@
+"""GPU parity of block eviction/restore (bit-exact round trips) and of the
+step-setup metadata kernels (slot mapping, page-index flattening)."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_offloading_amd import ops, workloads
+from helpers import randn_bf16, u16
+from oracle import kv_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _caches(layers, blocks, h, d, seed, gpu):
+    ks = [randn_bf16((blocks, 16, h, d), seed + 2 * i, device=gpu) for i in range(layers)]
+    vs = [randn_bf16((blocks, 16, h, d), seed + 2 * i + 1, device=gpu) for i in range(layers)]
+    return ks, vs
+
+
+def test_gather_scatter_blocks_vs_oracle(gpu):
+    ks, vs = _caches(1, 64, 16, 128, 1, gpu)
+    ids = np.array(workloads.randperm(64, 2)[:17], np.int32)
+    staging = torch.empty(17 * 2 * ops.block_bytes(ks[0]), dtype=torch.uint8, device=gpu)
+    ops.gather_blocks(ks[0], vs[0], torch.from_numpy(ids).to(gpu), staging)
+    ref = orc.gather_blocks(u16(ks[0]), u16(vs[0]), ids)
+    assert np.array_equal(staging.cpu().numpy().reshape(ref.shape), ref)
+    # scatter the staged image into other blocks
+    dst = np.array(workloads.randperm(64, 3)[:17], np.int32)
+    k2, v2 = _caches(1, 64, 16, 128, 50, gpu)
+    ek, ev = u16(k2[0]), u16(v2[0])
+    ops.scatter_blocks(staging, torch.from_numpy(dst).to(gpu), k2[0], v2[0])
+    orc.scatter_blocks(ref, dst, ek, ev)
+    assert np.array_equal(u16(k2[0]), ek) and np.array_equal(u16(v2[0]), ev)
+
+
+@pytest.mark.parametrize("staging_blocks", [1, 5, 1000])
+def test_swap_out_in_round_trip_bit_exact(gpu, staging_blocks):
+    layers, blocks, h, d = 3, 96, 16, 128
+    ks, vs = _caches(layers, blocks, h, d, 10, gpu)
+    snap = ([k.clone() for k in ks], [v.clone() for v in vs])
+    ids = torch.tensor(workloads.randperm(blocks, 4)[:24], dtype=torch.int32, device=gpu)
+    bb = ops.block_bytes(ks[0])
+    host = torch.empty(layers * 24 * 2 * bb, dtype=torch.uint8, pin_memory=True)
+    staging = torch.empty(staging_blocks * 2 * bb, dtype=torch.uint8, device=gpu)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    ops.swap_out_blocks(ks, vs, ids, host, staging, stream=side)
+    side.synchronize()
+    # the host image is the oracle's staging image, layer by layer
+    ref = np.concatenate([orc.gather_blocks(u16(k), u16(v), ids.cpu().numpy()).ravel()
+                          for k, v in zip(ks, vs)])
+    assert np.array_equal(host.numpy(), ref)
+    # clobber the evicted blocks, then restore into the same ids
+    for k, v in zip(ks, vs):
+        k[ids.long()] = 0
+        v[ids.long()] = 0
+    torch.cuda.synchronize()
+    ops.swap_in_blocks(host, ids, ks, vs, staging, stream=side)
+    side.synchronize()
+    for a, b in zip(ks + vs, snap[0] + snap[1]):
+        assert torch.equal(a, b)
+
+
+def test_swap_in_to_different_blocks(gpu):
+    layers, blocks = 2, 64
+    ks, vs = _caches(layers, blocks, 8, 128, 30, gpu)
+    perm = workloads.randperm(blocks, 5)
+    src = torch.tensor(perm[:10], dtype=torch.int32, device=gpu)
+    dst = torch.tensor(perm[10:20], dtype=torch.int32, device=gpu)
+    bb = ops.block_bytes(ks[0])
+    host = torch.empty(layers * 10 * 2 * bb, dtype=torch.uint8, pin_memory=True)
+    staging = torch.empty(4 * 2 * bb, dtype=torch.uint8, device=gpu)
+    before = [(k.clone(), v.clone()) for k, v in zip(ks, vs)]
+    ops.swap_out_blocks(ks, vs, src, host, staging)
+    ops.swap_in_blocks(host, dst, ks, vs, staging)
+    torch.cuda.synchronize()
+    untouched = torch.ones(blocks, dtype=torch.bool)
+    untouched[dst.long().cpu()] = False
+    for (k0, v0), k, v in zip(before, ks, vs):
+        assert torch.equal(k[dst.long()], k0[src.long()])
+        assert torch.equal(v[dst.long()], v0[src.long()])
+        assert torch.equal(k[untouched.to(gpu)], k0[untouched.to(gpu)])
+
+
+def test_swap_rejects_pageable_host_buffer(gpu):
+    ks, vs = _caches(1, 8, 8, 128, 40, gpu)
+    ids = torch.tensor([1, 2], dtype=torch.int32, device=gpu)
+    staging = torch.empty(2 * 2 * ops.block_bytes(ks[0]), dtype=torch.uint8, device=gpu)
+    with pytest.raises(RuntimeError):
+        ops.swap_out_blocks(ks, vs, ids, torch.empty(staging.numel(), dtype=torch.uint8), staging)
+
+
+def test_compute_slot_mapping_vs_oracle(gpu):
+    rng = np.random.default_rng(0)
+    max_seqs, width = 12, 40
+    pool = orc.FifoPagePool(400, max_seqs, width, free_order=workloads.randperm(400, 9))
+    computed = rng.integers(0, 300, max_seqs).astype(np.int32)
+    seq_ids = [3, 7, 0, 11, 5]
+    new = [1, 1, 37, 100, 16]  # two decode tokens, then prefill/continuation chunks
+    for s, n in zip(seq_ids, new):
+        pool.ensure_pages(s, (int(computed[s]) + n + 15) // 16)
+    graph_n = sum(new) + 9
+    ref_slots, ref_pos = orc.step_slot_mapping(pool.block_table, seq_ids, new, computed, graph_n)
+    qsl = np.zeros(len(new) + 1, np.int32)
+    np.cumsum(new, out=qsl[1:])
+    slots = torch.empty(graph_n, dtype=torch.int64, device=gpu)
+    pos = torch.empty(graph_n, dtype=torch.int32, device=gpu)
+    ops.compute_slot_mapping(torch.from_numpy(pool.block_table).to(gpu),
+                             torch.tensor(seq_ids, dtype=torch.int32, device=gpu),
+                             torch.from_numpy(qsl).to(gpu), torch.from_numpy(computed).to(gpu),
+                             sum(new), slots, pos)
+    assert np.array_equal(slots.cpu().numpy(), ref_slots)
+    assert np.array_equal(pos.cpu().numpy(), ref_pos)
+
+
+def test_copy_page_indices_vs_oracle(gpu):
+    max_seqs, width = 10, 300
+    pool = orc.FifoPagePool(2000, max_seqs, width, free_order=workloads.randperm(2000, 11))
+    lens = [5, 1000, 16, 4096, 1, 33]
+    seq_ids = [9, 2, 4, 0, 7, 3]
+    for s, ln in zip(seq_ids, lens):
+        pool.ensure_pages(s, (ln + 15) // 16)
+    indptr, _ = orc.plan_decode(lens)
+    ref = orc.page_indices(pool.block_table, seq_ids, indptr)
+    out = torch.full((int(indptr[-1]) + 5,), -7, dtype=torch.int32, device=gpu)
+    ops.copy_page_indices(torch.from_numpy(pool.block_table).to(gpu), torch.from_numpy(indptr).to(gpu),
+                          out, seq_ids=torch.tensor(seq_ids, dtype=torch.int32, device=gpu))
+    got = out.cpu().numpy()
+    assert np.array_equal(got[:-5], ref) and (got[-5:] == -7).all()
