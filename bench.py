@@ -1,0 +1,522 @@
+"""Benchmark of the paged KV-cache hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+
+A step is one Mixtral-8x7B-shaped decode step (configuration 2 of the
+benchmark set): 32 layers, 64 sequences with context uniform in [512, 4096],
+8 KV heads / 32 query heads, head_dim 128, 16-token pages from a seeded
+permuted pool.  Per step: the host setup (ensure_pages, device slot mapping,
+seq_lens += 1, decode plan with device page-index flattening) and, for each
+layer, the KV append of the 64 new tokens followed by paged decode attention
+over len + 1 tokens -- the engine's per-layer order (append inside stage 1,
+decode in stage 2).  Caches, queries and new K/V rows are resident in HBM
+before the timed region starts.
+
+``value`` is the step's algorithmic HBM bytes (decode: every K/V row read once
+per KV head + q in + out + page ids; append: rows read + written + slots)
+divided by the wall time of the step, so host setup and launch gaps count
+against it.  ``roofline`` is the decode-attention launch alone (partition +
+merge kernel, bracketed by HIP events on the stream they run on) against the
+8 TB/s HBM3E peak.  ``extra`` carries the other rows of the metric: chunked-
+prefill append and gather GB/s (configuration 3), long-context decode GB/s
+(configuration 4) and swap host-link GB/s with decode slowdown
+(configuration 5).  ``cpu_baseline`` times the numpy oracle on one layer of
+the same workload on the host cores.
+
+Other modes used by the profiles:
+  --mode copy     a plain device copy of known size (FETCH/WRITE calibration)
+  --mode decode4  configuration 4 decode only (32 launches)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-extra", action="store_true", help="skip configurations 3-5")
+    p.add_argument("--mode", default="step", choices=["step", "copy", "decode4"])
+    return p.parse_args()
+
+
+# --------------------------------------------------------------- helpers
+def _events(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def _fill_normal(t, std=1.0):
+    """In-place N(0, std^2) bf16 fill on the device (chunked, no fp32 copy)."""
+    flat = t.view(-1)
+    step = 1 << 28
+    for i in range(0, flat.numel(), step):
+        flat[i:i + step].normal_(0.0, std)
+
+
+def build_cfg2_cache(torch, seed, num_layers=None):
+    from gpu_offloading_amd import workloads
+    from gpu_offloading_amd.kv_cache import PagedKVCache
+
+    cfg = workloads.config2(seed=seed)
+    sh = cfg.shape
+    L = num_layers or sh.num_layers
+    B = len(cfg.seq_lens)
+    max_len = max(cfg.seq_lens) + cfg.extra["extra_steps"] + 16
+    cache = PagedKVCache(L, sh.num_kv_heads, sh.head_dim, max_seqs=B, max_seq_len=max_len,
+                         num_qo_heads=sh.num_qo_heads, kv_page_budget=cfg.total_pages,
+                         free_page_order=cfg.free_order, device="cuda")
+    seqs = list(range(B))
+    for s, ln in zip(seqs, cfg.seq_lens):
+        cache.ensure_pages(s, (ln + 15) // 16)
+    cache.advance(seqs, cfg.seq_lens)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 100)
+    for kc, vc in zip(cache.k_cache, cache.v_cache):
+        kc.normal_(0.0, 1.0, generator=g)
+        vc.normal_(0.0, 1.0, generator=g)
+    return cfg, cache, seqs
+
+
+# ------------------------------------------------------------ main step
+def run_step_bench(torch, args):
+    from gpu_offloading_amd import workloads
+
+    cfg, cache, seqs = build_cfg2_cache(torch, args.seed)
+    sh = cfg.shape
+    L, B = sh.num_layers, len(seqs)
+    dev = cache.device
+    g = torch.Generator(device="cuda")
+    g.manual_seed(args.seed + 200)
+    qs = [torch.randn(B, sh.num_qo_heads, sh.head_dim, device=dev, generator=g).to(torch.bfloat16)
+          for _ in range(L)]
+    ks = [torch.randn(B, sh.num_kv_heads, sh.head_dim, device=dev, generator=g).to(torch.bfloat16)
+          for _ in range(L)]
+    vs = [torch.randn(B, sh.num_kv_heads, sh.head_dim, device=dev, generator=g).to(torch.bfloat16)
+          for _ in range(L)]
+    outs = [torch.empty(B, sh.num_qo_heads, sh.head_dim, dtype=torch.bfloat16, device=dev)
+            for _ in range(L)]
+    total_steps = args.warmup + args.steps
+    if total_steps > cfg.extra["extra_steps"]:
+        raise SystemExit(f"warmup + steps must be <= {cfg.extra['extra_steps']} "
+                         "(page budget of the configuration)")
+
+    timed = {"on": False, "pairs": [], "bytes": 0, "decode_bytes": []}
+
+    def one_step():
+        lens_before = [int(cache._seq_lens_cpu[s]) for s in seqs]
+        for s, ln in zip(seqs, lens_before):            # scheduler: ensure_pages
+            cache.ensure_pages(s, (ln + 1 + 15) // 16)
+        slots = cache.prepare_decode_step(seqs)          # slot map, seq_lens += 1, plan
+        lens_after = [ln + 1 for ln in lens_before]
+        dbytes = workloads.decode_bytes(lens_after, sh.num_qo_heads, sh.num_kv_heads, sh.head_dim)
+        abytes = workloads.append_bytes(B, sh.num_kv_heads, sh.head_dim)
+        for layer in range(L):
+            cache.append(layer, ks[layer], vs[layer], slots)
+            if timed["on"]:
+                e0, e1 = _events(torch)
+                e0.record()
+                cache.decode(layer, qs[layer], out=outs[layer])
+                e1.record()
+                timed["pairs"].append((e0, e1))
+                timed["decode_bytes"].append(dbytes)
+            else:
+                cache.decode(layer, qs[layer], out=outs[layer])
+        if timed["on"]:
+            timed["bytes"] += L * (dbytes + abytes)
+
+    log(f"cfg2: {L} layers, B={B}, pages={cfg.total_pages}, warmup {args.warmup}, steps {args.steps}")
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    timed["on"] = True
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    step_gbps = timed["bytes"] / (t1 - t0) / 1e9
+    durs = [a.elapsed_time(b) for a, b in timed["pairs"]]  # ms
+    avg_ms = sum(durs) / len(durs)
+    avg_bytes = sum(timed["decode_bytes"]) / len(timed["decode_bytes"])
+    achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
+    sched = cache._decode_wrapper.schedule
+    log(f"cfg2: {ms_per_step:.3f} ms/step, step {step_gbps:.1f} GB/s, decode launch "
+        f"{avg_ms * 1e3:.1f} us = {achieved:.1f} GB/s ({achieved / HBM_PEAK_GBPS:.1%} of peak); "
+        f"ppp {sched.pages_per_partition}, parts {sched.max_partitions}")
+    # sanity: the outputs are finite
+    assert all(torch.isfinite(o.float()).all().item() for o in outs[:2]), "non-finite decode output"
+    res = {
+        "ms_per_step": ms_per_step,
+        "value": step_gbps,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": "decode_partition_kernel<4,128> + decode_merge_kernel<128>",
+                     "avg_launch_us": avg_ms * 1e3, "algorithmic_bytes_per_launch": avg_bytes,
+                     "pages_per_partition": sched.pages_per_partition,
+                     "max_partitions": sched.max_partitions},
+    }
+    del cache, qs, ks, vs, outs
+    torch.cuda.empty_cache()
+    return res
+
+
+# ----------------------------------------------------------- extras
+def run_cfg3(torch, seed, reps=10):
+    """Chunked-prefill append of 8 x 2048 tokens per layer into a pool whose
+    free list is a random 40% of its blocks, then gather of every sequence."""
+    from gpu_offloading_amd import ops, workloads
+    from gpu_offloading_amd.allocator import PagePool
+
+    cfg = workloads.config3(seed=seed)
+    sh = cfg.shape
+    L = sh.num_layers
+    pool = PagePool(cfg.total_pages, 8, 2048 // 16, free_order=cfg.free_order)
+    bt = torch.full((8, 128), -1, dtype=torch.int32)
+    for s in range(8):
+        _, pages = pool.alloc(s, 128)
+        bt[s] = torch.tensor(pages, dtype=torch.int32)
+    pos = torch.arange(2048)
+    slots = torch.cat([bt[s, pos // 16].long() * 16 + pos % 16 for s in range(8)]).cuda()
+    bt = bt.cuda()
+    n = slots.numel()
+    shape = (cfg.total_pages, 16, sh.num_kv_heads, sh.head_dim)
+    kcs = [torch.zeros(shape, dtype=torch.bfloat16, device="cuda") for _ in range(L)]
+    vcs = [torch.zeros(shape, dtype=torch.bfloat16, device="cuda") for _ in range(L)]
+    k = [torch.randn(n, sh.num_kv_heads, sh.head_dim, device="cuda").to(torch.bfloat16) for _ in range(2)]
+    v = [torch.randn(n, sh.num_kv_heads, sh.head_dim, device="cuda").to(torch.bfloat16) for _ in range(2)]
+    ok = torch.empty(n, sh.num_kv_heads, sh.head_dim, dtype=torch.bfloat16, device="cuda")
+    ov = torch.empty_like(ok)
+    cu = torch.arange(0, 9 * 2048, 2048, dtype=torch.int32, device="cuda")
+
+    def append_all(i):
+        for layer in range(L):
+            ops.reshape_and_cache_flash(k[i % 2], v[i % 2], kcs[layer], vcs[layer], slots)
+
+    def gather_all():
+        for layer in range(L):
+            ops.gather_kv(kcs[layer], vcs[layer], bt, cu, 2048, ok, ov)
+
+    append_all(0)
+    gather_all()
+    torch.cuda.synchronize()
+    e = _events(torch)
+    e[0].record()
+    for i in range(reps):
+        append_all(i)
+    e[1].record()
+    torch.cuda.synchronize()
+    t_app = e[0].elapsed_time(e[1]) * 1e-3 / (reps * L)
+    e[0].record()
+    for _ in range(reps):
+        gather_all()
+    e[1].record()
+    torch.cuda.synchronize()
+    t_gat = e[0].elapsed_time(e[1]) * 1e-3 / (reps * L)
+    ok_exact = bool(torch.equal(ok, k[(reps - 1) % 2]) and torch.equal(ov, v[(reps - 1) % 2]))
+    ab = workloads.append_bytes(n, sh.num_kv_heads, sh.head_dim)
+    gb = workloads.gather_bytes([2048] * 8, sh.num_kv_heads, sh.head_dim)
+    res = {"append_GBps": ab / t_app / 1e9, "append_us_per_layer": t_app * 1e6,
+           "gather_GBps": gb / t_gat / 1e9, "gather_us_per_layer": t_gat * 1e6,
+           "gather_roundtrip_bit_exact": ok_exact, "tokens_per_layer": n}
+    log(f"cfg3: append {res['append_GBps']:.0f} GB/s ({t_app * 1e6:.1f} us/layer), gather "
+        f"{res['gather_GBps']:.0f} GB/s ({t_gat * 1e6:.1f} us/layer), round trip exact {ok_exact}")
+    del kcs, vcs, k, v, ok, ov
+    torch.cuda.empty_cache()
+    return res
+
+
+def build_paged(torch, lens, hkv, d, seed, q_std=1.0, hq=32):
+    """Device caches holding sequences `lens` in a seeded permuted pool, plus
+    a planned decode wrapper."""
+    from gpu_offloading_amd import workloads
+    from gpu_offloading_amd.decode import BatchDecodeWithPagedKVCacheWrapper
+    import numpy as np
+
+    need = sum((ln + 15) // 16 for ln in lens)
+    total = need + 16
+    perm = np.asarray(workloads.randperm(total, seed), dtype=np.int32)
+    nblk = np.array([(ln + 15) // 16 for ln in lens])
+    indptr = np.zeros(len(lens) + 1, np.int32)
+    np.cumsum(nblk, out=indptr[1:])
+    indices = perm[:need].copy()
+    lpl = np.array([ln % 16 or 16 for ln in lens], np.int32)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    kc = torch.empty(total, 16, hkv, d, dtype=torch.bfloat16, device="cuda")
+    vc = torch.empty_like(kc)
+    kc.normal_(0, 1, generator=g)
+    vc.normal_(0, 1, generator=g)
+    q = (torch.randn(len(lens), hq, d, device="cuda", generator=g) * q_std).to(torch.bfloat16)
+    w = BatchDecodeWithPagedKVCacheWrapper(torch.empty(128 << 20, dtype=torch.uint8, device="cuda"))
+    w.plan(torch.from_numpy(indptr), torch.from_numpy(indices).cuda(), torch.from_numpy(lpl),
+           num_qo_heads=hq, num_kv_heads=hkv, head_dim=d, page_size=16)
+    return kc, vc, q, w
+
+
+def run_cfg4(torch, seed, reps=32):
+    from gpu_offloading_amd import workloads
+
+    cfg = workloads.config4(seed=seed)
+    sh = cfg.shape
+    kc, vc, q, w = build_paged(torch, cfg.seq_lens, sh.num_kv_heads, sh.head_dim, seed + 5,
+                               q_std=cfg.q_std, hq=sh.num_qo_heads)
+    out = torch.empty_like(q)
+    w.run(q, (kc, vc), out=out)
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(reps):
+        w.run(q, (kc, vc), out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / reps
+    b = workloads.decode_bytes(cfg.seq_lens, sh.num_qo_heads, sh.num_kv_heads, sh.head_dim)
+    res = {"decode_GBps": b / t / 1e9, "decode_us": t * 1e6, "frac_of_peak": b / t / 1e9 / HBM_PEAK_GBPS,
+           "pages_per_partition": w.schedule.pages_per_partition}
+    log(f"cfg4: decode {res['decode_GBps']:.0f} GB/s ({t * 1e6:.1f} us, "
+        f"{res['frac_of_peak']:.1%} of peak)")
+    del kc, vc, q, w, out
+    torch.cuda.empty_cache()
+    return res
+
+
+def run_cfg5(torch, seed, decode_steps=6):
+    """OLMoE-shaped swap under load: 16 layers, Hkv = Hq = 16, batch 128 at
+    2048 tokens; a seeded 25% of the sequences are evicted to pinned host
+    memory and restored on the side stream while the other 96 decode."""
+    from gpu_offloading_amd import workloads
+    from gpu_offloading_amd.kv_cache import PagedKVCache
+
+    cfg = workloads.config5(seed=seed)
+    sh = cfg.shape
+    L, B = sh.num_layers, len(cfg.seq_lens)
+    cache = PagedKVCache(L, sh.num_kv_heads, sh.head_dim, max_seqs=B, max_seq_len=2048 + 64,
+                         num_qo_heads=sh.num_qo_heads, kv_page_budget=cfg.total_pages,
+                         free_page_order=cfg.free_order, device="cuda",
+                         staging_bytes=512 << 20)
+    seqs = list(range(B))
+    for s in seqs:
+        cache.ensure_pages(s, 2048 // 16)
+    cache.advance(seqs, cfg.seq_lens)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 300)
+    for kc, vc in zip(cache.k_cache, cache.v_cache):
+        kc.normal_(0, 1, generator=g)
+        vc.normal_(0, 1, generator=g)
+    victims = sorted(workloads.randperm(B, seed + 7)[: B // 4])
+    running = [s for s in seqs if s not in set(victims)]
+    q = torch.randn(len(running), sh.num_qo_heads, sh.head_dim, device="cuda",
+                    generator=g).to(torch.bfloat16)
+    out = torch.empty_like(q)
+
+    def decode_pass():
+        cache.plan_decode(running)
+        for layer in range(L):
+            cache.decode(layer, q, out=out)
+
+    # reference snapshot of the victims' blocks (device gather, compared after)
+    before = cache.gather(0, victims)
+    before_last = cache.gather(L - 1, victims)
+    decode_pass()
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(decode_steps):
+        decode_pass()
+    e1.record()
+    torch.cuda.synchronize()
+    t_alone = e0.elapsed_time(e1) * 1e-3 / decode_steps
+
+    # pinned host buffer allocated up front (hipHostMalloc of 8 GiB is not link time)
+    bb = 2 * cache.k_cache[0][0].numel() * cache.k_cache[0].element_size()
+    npages = sum(cache.seq_pages(s) for s in victims)
+    host = torch.empty(L * npages * bb, dtype=torch.uint8, pin_memory=True)
+
+    # swap out under load: decode steps of the running sequences keep being
+    # issued on the current stream until the side stream has finished
+    h = cache.swap_out(victims, host=host)
+    e0.record()
+    n_dec = 0
+    while not h.out_event.query():
+        decode_pass()
+        n_dec += 1
+        torch.cuda.current_stream().synchronize()
+    e1.record()
+    h.out_event.synchronize()
+    torch.cuda.synchronize()
+    t_out = h.out_seconds()
+    t_dec_out = e0.elapsed_time(e1) * 1e-3 / max(n_dec, 1)
+
+    cache.swap_in(h)
+    n_dec_in = 0
+    e0.record()
+    while not h.in_event.query():
+        decode_pass()
+        n_dec_in += 1
+        torch.cuda.current_stream().synchronize()
+    e1.record()
+    h.in_event.synchronize()
+    torch.cuda.synchronize()
+    t_in = h.in_seconds()
+    t_dec_in = e0.elapsed_time(e1) * 1e-3 / max(n_dec_in, 1)
+    after = cache.gather(0, victims)
+    after_last = cache.gather(L - 1, victims)
+    exact = all(torch.equal(a, b) for a, b in zip(before + before_last, after + after_last))
+    nbytes = h.bytes_per_direction
+    res = {"swap_out_GBps": nbytes / t_out / 1e9, "swap_in_GBps": nbytes / t_in / 1e9,
+           "bytes_each_way": nbytes, "blocks": h.num_blocks * L,
+           "decode_ms_alone": t_alone * 1e3,
+           "decode_ms_during_swap_out": t_dec_out * 1e3 if n_dec else None,
+           "decode_ms_during_swap_in": t_dec_in * 1e3 if n_dec_in else None,
+           "decode_steps_during_swap": n_dec + n_dec_in,
+           "restored_bit_exact": bool(exact)}
+    sl = [x for x in (res["decode_ms_during_swap_out"], res["decode_ms_during_swap_in"]) if x]
+    res["decode_slowdown"] = (sum(sl) / len(sl)) / res["decode_ms_alone"] if sl else None
+    log(f"cfg5: swap out {res['swap_out_GBps']:.1f} GB/s, in {res['swap_in_GBps']:.1f} GB/s "
+        f"({nbytes / 1e9:.2f} GB each way), decode slowdown {res['decode_slowdown']}, "
+        f"restored exact {exact}")
+    cache.synchronize_swaps()
+    del cache, q, out, before, after, before_last, after_last, h
+    torch.cuda.empty_cache()
+    return res
+
+
+# ----------------------------------------------------------- CPU baseline
+def run_cpu_baseline(seed, reps=3):
+    """The numpy oracle (the CPU restatement of the reference path) on one
+    layer of configuration 2: append of the 64 new tokens, then fp32 decode
+    attention over len + 1 tokens of all 64 sequences; single-threaded."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from gpu_offloading_amd import workloads
+    from oracle import kv_oracle as orc
+
+    cfg = workloads.config2(seed=seed)
+    sh = cfg.shape
+    lens = list(cfg.seq_lens)
+    B = len(lens)
+    rng = np.random.default_rng(seed)
+    pool = orc.FifoPagePool(cfg.total_pages, B, max(lens) // 16 + 8, free_order=cfg.free_order)
+    for s, ln in enumerate(lens):
+        pool.ensure_pages(s, (ln + 1 + 15) // 16)
+
+    def rand_bf16(shape):
+        return orc.f32_to_bf16(rng.standard_normal(shape, dtype=np.float32))
+
+    kc = rand_bf16((cfg.total_pages, 16, sh.num_kv_heads, sh.head_dim))
+    vc = rand_bf16((cfg.total_pages, 16, sh.num_kv_heads, sh.head_dim))
+    kn = rand_bf16((B, sh.num_kv_heads, sh.head_dim))
+    vn = rand_bf16((B, sh.num_kv_heads, sh.head_dim))
+    q = rand_bf16((B, sh.num_qo_heads, sh.head_dim))
+    lens1 = [ln + 1 for ln in lens]
+    slots = orc.slot_mapping(pool.block_table, range(B), lens)
+    indptr, lpl = orc.plan_decode(lens1)
+    indices = orc.page_indices(pool.block_table, range(B), indptr)
+    nbytes = (workloads.decode_bytes(lens1, sh.num_qo_heads, sh.num_kv_heads, sh.head_dim)
+              + workloads.append_bytes(B, sh.num_kv_heads, sh.head_dim))
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            orc.reshape_and_cache(kn, vn, kc, vc, slots)
+            orc.paged_decode(q, kc, vc, indptr, indices, lpl)
+        dt = time.perf_counter() - t0
+    gbps = nbytes * reps / dt / 1e9
+    log(f"cpu baseline: {gbps:.3f} GB/s over {dt:.1f} s")
+    return {"value": gbps, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle, 1 layer of cfg2 (64 seqs, append 64 tokens + fp32 decode "
+                      f"over len+1), x{reps}, {dt:.1f} s, 1 thread",
+            "seconds": dt}
+
+
+# --------------------------------------------------------------- modes
+def run_copy_calibration(torch):
+    """A plain device-to-device copy of 1 GiB, x5: the FETCH_SIZE /
+    WRITE_SIZE calibration for the counter-based traffic figure."""
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "copy", "bytes_read": n, "bytes_written": n, "launches": 5}), flush=True)
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the paged KV-cache path has no "
+              "cross-GPU exchange and this build runs on a single MI355X "
+              f"(asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (no CPU fallback)", file=sys.stderr)
+        sys.exit(1)
+    from gpu_offloading_amd import _lib
+
+    _lib.load()
+    torch.cuda.set_device(0)
+    if args.mode == "copy":
+        run_copy_calibration(torch)
+        return
+    if args.mode == "decode4":
+        run_cfg4(torch, args.seed)
+        return
+
+    res = run_step_bench(torch, args)
+    extra = {}
+    if not args.no_extra:
+        extra["cfg3_chunked_prefill"] = run_cfg3(torch, args.seed)
+        extra["cfg4_long_context"] = run_cfg4(torch, args.seed)
+        extra["cfg5_swap"] = run_cfg5(torch, args.seed)
+    cpu = None if args.no_cpu else run_cpu_baseline(args.seed)
+    line = {
+        "metric": "paged decode-attn HBM GB/s (% peak) + KV append/gather/swap GB/s, 1 GPU",
+        "value": round(res["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V/Q, seeded permuted page pool)",
+        "config": {"workload": "cfg2 Mixtral-8x7B-shaped decode step: 32 layers x (append 64 tokens "
+                               "+ paged GQA decode), B=64, ctx U[512,4096], Hkv=8, Hq=32, D=128, "
+                               "page 16, bf16; value = (decode + append algorithmic bytes) / step "
+                               "wall time incl. host setup",
+                   "global_batch": 64, "layers": 32, "parallelism": "none (1 GPU)"},
+        "roofline": res["roofline"],
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

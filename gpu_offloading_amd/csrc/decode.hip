@@ -8,24 +8,37 @@
 // head hq / group.  Split-K partials are merged with the log-sum-exp rule of
 // src/dense/offload_kv_attn.py:24-39 (done in base 2 here).
 //
-// Decode is a GEMV: every K/V byte is used by `group` query heads only, so the
-// kernel is HBM-bound and runs on the VALU (no MFMA):
-//   * grid (max_partitions, num_kv_heads, batch); a 256-thread workgroup owns
-//     one (request, KV head, partition of pages_per_partition pages) and serves
-//     all `group` query heads of that KV head, so K/V are read exactly once;
-//   * each wave streams every 4th page of the partition.  A page holds 16 token
-//     rows of 256 B per KV head (head_dim 128, bf16); lane (row r, column c)
-//     loads 16 B (dims 8c..8c+7) of tokens r, r+4, r+8, r+12 for K and for V,
-//     i.e. eight global_load_dwordx4 per lane per page, fully coalesced in 256 B
-//     runs.  The next page is prefetched into a second register set while the
-//     current one is consumed;
-//   * q.k uses v_dot2c_f32_bf16 on the raw bf16 pairs (exact products, fp32
-//     sum); the 16 lanes of a DPP row are reduced with quad_perm/row_ror DPP
-//     adds; each row keeps its own online-softmax state (m, l, acc) in base 2;
-//   * epilogue: rows merge with lane shuffles, the four waves merge through
-//     LDS, and the workgroup writes either the final bf16 output (single
-//     partition) or an fp32 partial + its log2-sum-exp to the workspace, which
-//     decode_merge_kernel folds.
+// Decode is a GEMV: every K/V byte feeds only `group` query heads, so the
+// kernels are HBM-bound and run on the VALU (no MFMA).  Work decomposition:
+//   * grid (num_kv_heads, max_partitions, batch), KV head fastest: the
+//     workgroups of the heads of one page range are dispatched together (to
+//     the eight XCDs in turn), so the 2 KB token rows of a page are read by
+//     concurrent workgroups, and every XCD receives the same share of work
+//     whatever the spread of request lengths;
+//   * a 256-thread workgroup owns one (request, KV head, partition of
+//     pages_per_partition pages) and serves all `group` query heads of that KV
+//     head, so K/V are read from HBM exactly once; wave w takes pages
+//     p0 + w, p0 + w + 4, ...  Each wave's page ids are loaded once, one per
+//     lane, and broadcast with v_readlane, so no dependent global load sits
+//     in the streaming loop;
+//   * epilogue: the four waves merge through LDS; a request with one partition
+//     is written as bf16 directly, otherwise an fp32 partial + log2-sum-exp
+//     goes to the workspace and decode_merge_kernel folds them.
+//
+// head_dim 128 (the reference models) uses decode_lds_kernel: each wave stages
+// one page (16 tokens x 256 B of K and of V) from HBM through registers into
+// its own 8 KB LDS tile while the previous page is being consumed.  The tile
+// is stored with the 16-byte chunk c of token t at slot c ^ t, which makes
+// both read patterns below free of LDS bank conflicts:
+//   q.k : lane (token t, query head g) computes the whole 128-dim dot product
+//         with v_dot2_f32_bf16 from 16 ds_read_b128 of row t (the four lanes
+//         of a token read the same address); no cross-lane reduction;
+//   p.v : lane l owns dims 2l, 2l+1 for every query head; per token one
+//         ds_read_b32 of V and one broadcast read of p[t][0..G).
+// Softmax statistics live per 16-lane DPP row (one query head per row).
+// head_dim 64 and 256 use decode_reg_kernel, which keeps K/V in registers:
+// lane (row r, column c) holds 16 B of tokens r, r+4, r+8, r+12 and q.k is
+// reduced over the 16 lanes of a DPP row.
 #include "kvc_common.h"
 
 #include <algorithm>
@@ -37,7 +50,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kPage = 16;      // tokens per page (the engine's page_size)
-constexpr int kTokPerRow = 4;  // tokens of a page handled by one 16-lane row
+constexpr int kTokPerRow = 4;  // register kernel: tokens of a page per 16-lane row
+constexpr int kMaxPagesPerPart = 4 * 64;  // a wave holds its page ids in 64 lanes
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kLog2e = 1.44269504088896340736f;
 
@@ -64,22 +78,302 @@ struct DecodeArgs {
   float* lse;              // [batch][Hq] natural log, may be null
 };
 
+// Compiler-level ordering point for LDS traffic between lanes of one wave
+// (the LDS unit itself executes one wave's instructions in order).
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<kDppQuadSwap1>(v));
+  v = fmaxf(v, dpp<kDppQuadSwap2>(v));
+  v = fmaxf(v, dpp<kDppRowRor4>(v));
+  v = fmaxf(v, dpp<kDppRowRor8>(v));
+  return v;
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Page ids of the calling wave: lane j holds the block id of the wave's j-th
+// page (page p0 + wave + 4j of the request), -1 past the end.
+__device__ __forceinline__ int32_t load_wave_page_ids(const DecodeArgs& a, int pbeg,
+                                                      int first, int nw, int lane) {
+  int32_t id = -1;
+  if (lane < nw) {
+    const int64_t slot = int64_t(pbeg) + first + int64_t(kWaves) * lane;
+    id = slot < a.num_indices ? a.indices[slot] : -1;
+  }
+  return id;
+}
+
+// Wave-merge + output.  s_acc [kWaves][G][D], s_m / s_l [kWaves][G] hold each
+// wave's unnormalised accumulator and base-2 softmax statistics.
+template <int G, int D>
+__device__ __forceinline__ void finish_partition(const DecodeArgs& a, int b, int h, int part,
+                                                 int nparts, const float* s_acc,
+                                                 const float* s_m, const float* s_l) {
+  const int hq0 = h * G;
+  const int64_t part_base = (int64_t(b) * a.num_kv_heads + h) * a.max_parts + part;
+  for (int o = threadIdx.x; o < G * D; o += kThreads) {
+    const int g = o / D;
+    const int d = o - g * D;
+    float mm = kNegBig;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, s_m[w * G + g]);
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = fast_exp2(s_m[w * G + g] - mm);
+      L = fmaf(s_l[w * G + g], f, L);
+      A = fmaf(s_acc[(w * G + g) * D + d], f, A);
+    }
+    const float res = L > 0.f ? A / L : 0.f;
+    const float lse2 = L > 0.f ? mm + fast_log2(L) : -INFINITY;
+    if (nparts == 1) {
+      a.out[int64_t(b) * a.out_stride + int64_t(hq0 + g) * D + d] = f32_to_bf16(res);
+      if (a.lse && d == 0)
+        a.lse[int64_t(b) * a.num_kv_heads * G + hq0 + g] = lse2 * kLn2;
+    } else {
+      a.part_o[(part_base * G + g) * D + d] = res;
+      if (d == 0) a.part_lse[part_base * G + g] = lse2;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// head_dim 128: LDS-staged kernel.
+// ---------------------------------------------------------------------------
+template <int G>
+struct LdsCfg {
+  static constexpr int QL = G > 4 ? G / 4 : 1;  // query heads per lane in q.k
+  static constexpr int GP = G < 4 ? G : 4;      // distinct query heads over the 4 rows
+  static constexpr int NS = G < 4 ? 4 / G : 1;  // lanes sharing one dot product
+  static constexpr int CH = 16 / NS;            // 16-byte chunks of a K row per lane
+};
+
+struct __align__(16) PageTile {
+  uint4 k[kPage * 16];  // [token][slot], slot = chunk ^ token
+  uint4 v[kPage * 16];
+  float p[kPage * 8];   // softmax weights p[token][query head], G <= 8
+};
+
+template <int G>
+__global__ __launch_bounds__(kThreads) void decode_lds_kernel(DecodeArgs a) {
+  using C = LdsCfg<G>;
+  constexpr int D = 128;
+  __shared__ PageTile s_tile[kWaves];
+  static_assert(sizeof(s_tile) >= sizeof(float) * (kWaves * G * D + 2 * kWaves * G),
+                "epilogue does not fit in the page tiles");
+
+  const int h = blockIdx.x;
+  const int part = blockIdx.y;
+  const int b = blockIdx.z;
+  const int pbeg = a.indptr[b];
+  const int npages = a.indptr[b + 1] - pbeg;
+  const int p0 = part * a.pages_per_part;
+  if (p0 >= npages) return;  // uniform over the workgroup
+  const int p1 = min(p0 + a.pages_per_part, npages);
+  const int nparts = (npages + a.pages_per_part - 1) / a.pages_per_part;
+  const int last_len = min(max(a.last_page_len[b], 0), kPage);
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  PageTile& tile = s_tile[wave];
+
+  // q.k role: token t, query head gq (and gq + 4 when G == 8), dim split.
+  const int t = lane & 15;
+  const int row = lane >> 4;
+  const int gq = row % C::GP;
+  const int split = row / C::GP;
+  uint32_t qw[C::QL][C::CH * 4];
+#pragma unroll
+  for (int ql = 0; ql < C::QL; ++ql) {
+    const uint4* qp = reinterpret_cast<const uint4*>(
+        a.q + int64_t(b) * a.q_stride + int64_t(h * G + gq + 4 * ql) * D + split * C::CH * 8);
+#pragma unroll
+    for (int i = 0; i < C::CH; ++i) {
+      const uint4 x = qp[i];
+      qw[ql][4 * i + 0] = x.x;
+      qw[ql][4 * i + 1] = x.y;
+      qw[ql][4 * i + 2] = x.z;
+      qw[ql][4 * i + 3] = x.w;
+    }
+  }
+  // Staging role: load instruction u moves tokens 4u..4u+3; lane -> (token, slot).
+  const int st_tok = lane >> 4;
+  const int st_slot = lane & 15;
+  int32_t st_off[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int tok = 4 * u + st_tok;
+    st_off[u] = int32_t(tok * a.token_stride) + h * D + ((st_slot ^ tok) << 3);
+  }
+  // p.v role: dims 2*lane, 2*lane+1 = word lane&3 of chunk lane>>2.
+  const int vchunk = lane >> 2;
+  const int vword = lane & 3;
+
+  const int nw = p1 - p0 > wave ? (p1 - p0 - wave + kWaves - 1) / kWaves : 0;
+  const int32_t my_ids = load_wave_page_ids(a, pbeg, p0 + wave, nw, lane);
+
+  float m_run[C::QL], l_run[C::QL], acc[G][2];
+#pragma unroll
+  for (int ql = 0; ql < C::QL; ++ql) {
+    m_run[ql] = kNegBig;
+    l_run[ql] = 0.f;
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
+
+  uint4 rk[4], rv[4];
+  auto issue = [&](int32_t blk) {
+    const int64_t base = int64_t(blk) * a.block_stride;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      rk[u] = *reinterpret_cast<const uint4*>(a.k_cache + base + st_off[u]);
+      rv[u] = *reinterpret_cast<const uint4*>(a.v_cache + base + st_off[u]);
+    }
+  };
+  auto safe_id = [&](int32_t id) { return (id >= 0 && id < a.num_blocks) ? id : 0; };
+
+  int32_t blk = nw > 0 ? __builtin_amdgcn_readlane(my_ids, 0) : 0;
+  if (nw > 0) issue(safe_id(blk));
+  for (int j = 0; j < nw; ++j) {
+    const int pi = p0 + wave + kWaves * j;
+    const bool blk_ok = blk >= 0 && blk < a.num_blocks;
+    const int valid = !blk_ok ? 0 : (pi == npages - 1 ? last_len : kPage);
+    if (valid < kPage) {
+      // Rows past the end may hold anything (even NaN bits): stage zeros so
+      // that 0 * v stays 0.
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (4 * u + st_tok >= valid) rk[u] = rv[u] = make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      tile.k[u * 64 + lane] = rk[u];
+      tile.v[u * 64 + lane] = rv[u];
+    }
+    if (j + 1 < nw) {
+      blk = __builtin_amdgcn_readlane(my_ids, j + 1);
+      issue(safe_id(blk));  // in flight while this page is consumed
+    }
+    wave_lds_fence();
+
+    // q.k: lane (t, gq) over its chunks of K row t.
+    float dots[C::QL];
+#pragma unroll
+    for (int ql = 0; ql < C::QL; ++ql) dots[ql] = 0.f;
+    const uint4* krow = tile.k + t * 16;
+#pragma unroll
+    for (int i = 0; i < C::CH; ++i) {
+      const int c = split * C::CH + i;
+      const uint4 kv = krow[c ^ t];
+#pragma unroll
+      for (int ql = 0; ql < C::QL; ++ql) {
+        dots[ql] = dot2_bf16(qw[ql][4 * i + 0], kv.x, dots[ql]);
+        dots[ql] = dot2_bf16(qw[ql][4 * i + 1], kv.y, dots[ql]);
+        dots[ql] = dot2_bf16(qw[ql][4 * i + 2], kv.z, dots[ql]);
+        dots[ql] = dot2_bf16(qw[ql][4 * i + 3], kv.w, dots[ql]);
+      }
+    }
+#pragma unroll
+    for (int off = 16 * C::GP; off < 64; off <<= 1)
+#pragma unroll
+      for (int ql = 0; ql < C::QL; ++ql) dots[ql] += __shfl_xor(dots[ql], off);
+
+    // Online softmax per row (one query head per 16-lane row).
+    const bool live = t < valid;
+    float alpha[C::QL];
+#pragma unroll
+    for (int ql = 0; ql < C::QL; ++ql) {
+      const float s = live ? dots[ql] * a.scale_log2 : kNegBig;
+      const float m_new = fmaxf(m_run[ql], row16_max(s));
+      const float p = live ? fast_exp2(s - m_new) : 0.f;
+      alpha[ql] = fast_exp2(m_run[ql] - m_new);
+      l_run[ql] = fmaf(l_run[ql], alpha[ql], row16_sum(p));
+      m_run[ql] = m_new;
+      if (row < C::GP) tile.p[t * G + gq + 4 * ql] = p;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float al = readlane_f(alpha[g / 4], 16 * (g % 4));
+      acc[g][0] *= al;
+      acc[g][1] *= al;
+    }
+    wave_lds_fence();
+
+    // p.v over the 16 tokens of the page (rows past `valid` are zero).
+    const char* vbase = reinterpret_cast<const char*>(tile.v) + vword * 4;
+#pragma unroll
+    for (int tt = 0; tt < kPage; ++tt) {
+      const uint32_t vw =
+          *reinterpret_cast<const uint32_t*>(vbase + tt * 256 + ((vchunk ^ tt) << 4));
+      const float v0 = bf16lo(vw);
+      const float v1 = bf16hi(vw);
+      float pg[G];
+      if constexpr (G >= 4) {
+#pragma unroll
+        for (int q4 = 0; q4 < G / 4; ++q4) {
+          const float4 x = reinterpret_cast<const float4*>(tile.p + tt * G)[q4];
+          pg[4 * q4 + 0] = x.x;
+          pg[4 * q4 + 1] = x.y;
+          pg[4 * q4 + 2] = x.z;
+          pg[4 * q4 + 3] = x.w;
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) pg[g] = tile.p[tt * G + g];
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        acc[g][0] = fmaf(pg[g], v0, acc[g][0]);
+        acc[g][1] = fmaf(pg[g], v1, acc[g][1]);
+      }
+    }
+    wave_lds_fence();
+  }
+
+  // Workgroup epilogue (the page tiles are reused for the wave partials).
+  __syncthreads();
+  float* s_acc = reinterpret_cast<float*>(s_tile);
+  float* s_m = s_acc + kWaves * G * D;
+  float* s_l = s_m + kWaves * G;
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    *reinterpret_cast<float2*>(s_acc + (wave * G + g) * D + 2 * lane) =
+        make_float2(acc[g][0], acc[g][1]);
+  if (t == 0 && row < C::GP) {
+#pragma unroll
+    for (int ql = 0; ql < C::QL; ++ql) {
+      s_m[wave * G + gq + 4 * ql] = m_run[ql];
+      s_l[wave * G + gq + 4 * ql] = l_run[ql];
+    }
+  }
+  __syncthreads();
+  finish_partition<G, D>(a, b, h, part, nparts, s_acc, s_m, s_l);
+}
+
+// ---------------------------------------------------------------------------
+// head_dim 64 / 256: register kernel.
+// ---------------------------------------------------------------------------
 // Load the D/16 bf16 elements one lane owns (D/32 32-bit words).
 template <int D>
-__device__ __forceinline__ void load_slice(uint32_t (&w)[D / 32],
-                                           const uint16_t* p) {
+__device__ __forceinline__ void load_slice(uint32_t (&w)[D / 32], const uint16_t* p) {
   if constexpr (D == 64) {
-    const uint2 t = *reinterpret_cast<const uint2*>(p);
-    w[0] = t.x; w[1] = t.y;
-  } else if constexpr (D == 128) {
-    const uint4 t = *reinterpret_cast<const uint4*>(p);
-    w[0] = t.x; w[1] = t.y; w[2] = t.z; w[3] = t.w;
+    const uint2 x = *reinterpret_cast<const uint2*>(p);
+    w[0] = x.x; w[1] = x.y;
   } else {
-    static_assert(D == 256, "head_dim must be 64, 128 or 256");
-    const uint4 t0 = reinterpret_cast<const uint4*>(p)[0];
-    const uint4 t1 = reinterpret_cast<const uint4*>(p)[1];
-    w[0] = t0.x; w[1] = t0.y; w[2] = t0.z; w[3] = t0.w;
-    w[4] = t1.x; w[5] = t1.y; w[6] = t1.z; w[7] = t1.w;
+    static_assert(D == 128 || D == 256, "head_dim must be 64, 128 or 256");
+#pragma unroll
+    for (int i = 0; i < D / 128; ++i) {
+      const uint4 x = reinterpret_cast<const uint4*>(p)[i];
+      w[4 * i + 0] = x.x; w[4 * i + 1] = x.y; w[4 * i + 2] = x.z; w[4 * i + 3] = x.w;
+    }
   }
 }
 
@@ -89,53 +383,32 @@ struct PageRegs {
   uint32_t v[kTokPerRow][D / 32];
 };
 
-// Issue the loads of page `pi` (index into this request's page list) and
-// return its number of valid tokens (0 for an out-of-range block id).
 template <int D>
-__device__ __forceinline__ int load_page(const DecodeArgs& a, PageRegs<D>& r,
-                                         int64_t page_slot, int valid_tokens,
-                                         int64_t lane_off) {
-  int32_t blk = page_slot < a.num_indices ? a.indices[page_slot] : -1;
-  if (blk < 0 || blk >= a.num_blocks) {
-#pragma unroll
-    for (int j = 0; j < kTokPerRow; ++j)
-#pragma unroll
-      for (int w = 0; w < D / 32; ++w) r.k[j][w] = r.v[j][w] = 0u;
-    return 0;
-  }
+__device__ __forceinline__ void load_page_regs(const DecodeArgs& a, PageRegs<D>& r,
+                                               int32_t blk, int64_t lane_off) {
   const int64_t base = int64_t(blk) * a.block_stride + lane_off;
-  const uint16_t* kp = a.k_cache + base;
-  const uint16_t* vp = a.v_cache + base;
 #pragma unroll
   for (int j = 0; j < kTokPerRow; ++j)
-    load_slice<D>(r.k[j], kp + int64_t(j) * kTokPerRow * a.token_stride);
+    load_slice<D>(r.k[j], a.k_cache + base + int64_t(j) * kTokPerRow * a.token_stride);
 #pragma unroll
   for (int j = 0; j < kTokPerRow; ++j)
-    load_slice<D>(r.v[j], vp + int64_t(j) * kTokPerRow * a.token_stride);
-  return valid_tokens;
+    load_slice<D>(r.v[j], a.v_cache + base + int64_t(j) * kTokPerRow * a.token_stride);
 }
 
 // Fold one page into the row's online-softmax state.
 template <int G, int D>
-__device__ __forceinline__ void consume_page(const uint32_t (&qw)[G][D / 32],
-                                             PageRegs<D>& r, int valid, int row,
-                                             float scale_log2, float (&m)[G],
-                                             float (&l)[G],
-                                             float (&acc)[G][D / 16]) {
+__device__ __forceinline__ void consume_page_regs(const uint32_t (&qw)[G][D / 32],
+                                                  PageRegs<D>& r, int valid, int row,
+                                                  float scale_log2, float (&m)[G],
+                                                  float (&l)[G], float (&acc)[G][D / 16]) {
   constexpr int W = D / 32;
-  bool ok[kTokPerRow];
-#pragma unroll
-  for (int j = 0; j < kTokPerRow; ++j) ok[j] = row + kTokPerRow * j < valid;
   if (valid < kPage) {
-    // Stale slots past the sequence end may hold anything (even NaN bits):
-    // clear their V so that 0 * v stays 0.
 #pragma unroll
     for (int j = 0; j < kTokPerRow; ++j)
-      if (!ok[j])
+      if (row + kTokPerRow * j >= valid)
 #pragma unroll
         for (int w = 0; w < W; ++w) r.v[j][w] = 0u;
   }
-
   float s[kTokPerRow][G];
 #pragma unroll
   for (int j = 0; j < kTokPerRow; ++j)
@@ -144,29 +417,27 @@ __device__ __forceinline__ void consume_page(const uint32_t (&qw)[G][D / 32],
       float d = 0.f;
 #pragma unroll
       for (int w = 0; w < W; ++w) d = dot2_bf16(qw[g][w], r.k[j][w], d);
-      s[j][g] = row16_sum(d) * scale_log2;
+      d = row16_sum(d) * scale_log2;
+      s[j][g] = row + kTokPerRow * j < valid ? d : kNegBig;
     }
-
-  float p[kTokPerRow][G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    float mx = kNegBig;
+    float mx = s[0][g];
 #pragma unroll
-    for (int j = 0; j < kTokPerRow; ++j) mx = ok[j] ? fmaxf(mx, s[j][g]) : mx;
+    for (int j = 1; j < kTokPerRow; ++j) mx = fmaxf(mx, s[j][g]);
     const float m_new = fmaxf(m[g], mx);
     const float alpha = fast_exp2(m[g] - m_new);
     float psum = 0.f;
 #pragma unroll
     for (int j = 0; j < kTokPerRow; ++j) {
-      p[j][g] = ok[j] ? fast_exp2(s[j][g] - m_new) : 0.f;
-      psum += p[j][g];
+      s[j][g] = row + kTokPerRow * j < valid ? fast_exp2(s[j][g] - m_new) : 0.f;
+      psum += s[j][g];
     }
-    l[g] = l[g] * alpha + psum;
+    l[g] = fmaf(l[g], alpha, psum);
     m[g] = m_new;
 #pragma unroll
     for (int e = 0; e < D / 16; ++e) acc[g][e] *= alpha;
   }
-
 #pragma unroll
   for (int j = 0; j < kTokPerRow; ++j)
 #pragma unroll
@@ -175,18 +446,21 @@ __device__ __forceinline__ void consume_page(const uint32_t (&qw)[G][D / 32],
       const float v1 = bf16hi(r.v[j][w]);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        acc[g][2 * w] = fmaf(p[j][g], v0, acc[g][2 * w]);
-        acc[g][2 * w + 1] = fmaf(p[j][g], v1, acc[g][2 * w + 1]);
+        acc[g][2 * w] = fmaf(s[j][g], v0, acc[g][2 * w]);
+        acc[g][2 * w + 1] = fmaf(s[j][g], v1, acc[g][2 * w + 1]);
       }
     }
 }
 
 template <int G, int D>
-__global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kThreads) void decode_reg_kernel(DecodeArgs a) {
   constexpr int W = D / 32;
   constexpr int E = D / 16;
-  const int part = blockIdx.x;
-  const int h = blockIdx.y;
+  __shared__ float s_acc[kWaves * G * D];
+  __shared__ float s_m[kWaves * G];
+  __shared__ float s_l[kWaves * G];
+  const int h = blockIdx.x;
+  const int part = blockIdx.y;
   const int b = blockIdx.z;
   const int pbeg = a.indptr[b];
   const int npages = a.indptr[b + 1] - pbeg;
@@ -217,23 +491,34 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
   }
 
   const int64_t lane_off = int64_t(row) * a.token_stride + int64_t(h) * D + col * E;
-  auto valid_of = [&](int pi) { return pi == npages - 1 ? last_len : kPage; };
+  const int nw = p1 - p0 > wave ? (p1 - p0 - wave + kWaves - 1) / kWaves : 0;
+  const int32_t my_ids = load_wave_page_ids(a, pbeg, p0 + wave, nw, lane);
+  auto id_at = [&](int j) { return __builtin_amdgcn_readlane(my_ids, j); };
+  auto safe = [&](int32_t id) { return (id >= 0 && id < a.num_blocks) ? id : 0; };
+  auto valid_at = [&](int j, int32_t id) {
+    if (id < 0 || id >= a.num_blocks) return 0;
+    return p0 + wave + kWaves * j == npages - 1 ? last_len : kPage;
+  };
 
-  // Two register sets: page pi is consumed while page pi+kWaves is in flight.
+  // Two register sets: page j is consumed while page j+1 is in flight.
   PageRegs<D> ra, rb;
-  int pi = p0 + wave;
-  int va = 0, vb = 0;
-  if (pi < p1) va = load_page<D>(a, ra, int64_t(pbeg) + pi, valid_of(pi), lane_off);
-  while (pi < p1) {
-    const int pn = pi + kWaves;
-    if (pn < p1) vb = load_page<D>(a, rb, int64_t(pbeg) + pn, valid_of(pn), lane_off);
-    consume_page<G, D>(qw, ra, va, row, a.scale_log2, m, l, acc);
-    pi = pn;
-    if (pi >= p1) break;
-    const int pn2 = pi + kWaves;
-    if (pn2 < p1) va = load_page<D>(a, ra, int64_t(pbeg) + pn2, valid_of(pn2), lane_off);
-    consume_page<G, D>(qw, rb, vb, row, a.scale_log2, m, l, acc);
-    pi = pn2;
+  int32_t ida = 0, idb = 0;
+  if (nw > 0) {
+    ida = id_at(0);
+    load_page_regs<D>(a, ra, safe(ida), lane_off);
+  }
+  for (int j = 0; j < nw; j += 2) {
+    if (j + 1 < nw) {
+      idb = id_at(j + 1);
+      load_page_regs<D>(a, rb, safe(idb), lane_off);
+    }
+    consume_page_regs<G, D>(qw, ra, valid_at(j, ida), row, a.scale_log2, m, l, acc);
+    if (j + 1 >= nw) break;
+    if (j + 2 < nw) {
+      ida = id_at(j + 2);
+      load_page_regs<D>(a, ra, safe(ida), lane_off);
+    }
+    consume_page_regs<G, D>(qw, rb, valid_at(j + 1, idb), row, a.scale_log2, m, l, acc);
   }
 
   // Merge the four rows of the wave (lanes c, c+16, c+32, c+48 hold the same dims).
@@ -255,52 +540,24 @@ __global__ __launch_bounds__(kThreads) void decode_partition_kernel(DecodeArgs a
       }
     }
   }
-
-  // Merge the waves through LDS.
-  __shared__ float s_acc[kWaves][G][D];
-  __shared__ float s_m[kWaves][G];
-  __shared__ float s_l[kWaves][G];
   if (row == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
 #pragma unroll
-      for (int e = 0; e < E; ++e) s_acc[wave][g][col * E + e] = acc[g][e];
+      for (int e = 0; e < E; ++e) s_acc[(wave * G + g) * D + col * E + e] = acc[g][e];
       if (col == 0) {
-        s_m[wave][g] = m[g];
-        s_l[wave][g] = l[g];
+        s_m[wave * G + g] = m[g];
+        s_l[wave * G + g] = l[g];
       }
     }
   }
   __syncthreads();
-
-  const int hq0 = h * G;
-  const int64_t part_base = (int64_t(b) * a.num_kv_heads + h) * a.max_parts + part;
-  for (int o = tid; o < G * D; o += kThreads) {
-    const int g = o / D;
-    const int d = o - g * D;
-    float mm = kNegBig;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, s_m[w][g]);
-    float L = 0.f, A = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float f = fast_exp2(s_m[w][g] - mm);
-      L = fmaf(s_l[w][g], f, L);
-      A = fmaf(s_acc[w][g][d], f, A);
-    }
-    const float res = L > 0.f ? A / L : 0.f;
-    const float lse2 = L > 0.f ? mm + fast_log2(L) : -INFINITY;
-    if (nparts == 1) {
-      a.out[int64_t(b) * a.out_stride + int64_t(hq0 + g) * D + d] = f32_to_bf16(res);
-      if (a.lse && d == 0)
-        a.lse[int64_t(b) * a.num_kv_heads * G + hq0 + g] = lse2 * kLn2;
-    } else {
-      a.part_o[(part_base * G + g) * D + d] = res;
-      if (d == 0) a.part_lse[part_base * G + g] = lse2;
-    }
-  }
+  finish_partition<G, D>(a, b, h, part, nparts, s_acc, s_m, s_l);
 }
 
+// ---------------------------------------------------------------------------
+// Split-K merge.
+// ---------------------------------------------------------------------------
 struct MergeArgs {
   const float* part_o;
   const float* part_lse;
@@ -314,13 +571,29 @@ struct MergeArgs {
   float* lse;
 };
 
-// Fold the partition partials of one (request, query head).  Requests with a
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// One wave per (request, query head): lane p reads the log2-sum-exp of
+// partition p, the wave forms the weights, then every lane folds its D/64
+// dims over the partitions (independent loads, unrolled).  Requests with a
 // single partition were finished by the partition kernel; requests with no
 // pages get a zero output and lse = -inf.
 template <int D>
 __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
+  constexpr int EPL = D / 64;  // dims per lane
   const int hq = blockIdx.x;
   const int b = blockIdx.y;
+  const int lane = threadIdx.x;
   const int G = a.group;
   const int npages = a.indptr[b + 1] - a.indptr[b];
   const int nparts = min(max((npages + a.pages_per_part - 1) / a.pages_per_part, 0),
@@ -331,32 +604,47 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
   const int h = hq / G;
   const int g = hq - h * G;
   const int64_t base = (int64_t(b) * a.num_kv_heads + h) * a.max_parts;
-  float mm = -INFINITY;
-  for (int p = 0; p < nparts; ++p) mm = fmaxf(mm, a.part_lse[(base + p) * G + g]);
-  if (nparts == 0 || mm == -INFINITY) {
-    for (int d = threadIdx.x; d < D; d += 64) out[d] = 0;
-    if (a.lse && threadIdx.x == 0) a.lse[int64_t(b) * Hq + hq] = -INFINITY;
+  const float* lp = a.part_lse + base * G + g;  // partition p at lp[p * G]
+
+  float mx = -INFINITY;
+  for (int p = lane; p < nparts; p += 64) mx = fmaxf(mx, lp[int64_t(p) * G]);
+  mx = wave_max(mx);
+  if (nparts == 0 || mx == -INFINITY) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) out[lane * EPL + e] = 0;
+    if (a.lse && lane == 0) a.lse[int64_t(b) * Hq + hq] = -INFINITY;
     return;
   }
+  float acc[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
   float S = 0.f;
-  for (int p = 0; p < nparts; ++p) S += fast_exp2(a.part_lse[(base + p) * G + g] - mm);
-  const float inv = 1.f / S;
-  for (int d = threadIdx.x; d < D; d += 64) {
-    float acc = 0.f;
-    for (int p = 0; p < nparts; ++p) {
-      const float w = fast_exp2(a.part_lse[(base + p) * G + g] - mm);
-      acc = fmaf(w, a.part_o[((base + p) * G + g) * D + d], acc);
+  for (int q0 = 0; q0 < nparts; q0 += 64) {
+    const float w = q0 + lane < nparts ? fast_exp2(lp[int64_t(q0 + lane) * G] - mx) : 0.f;
+    S += w;
+    const int n = min(64, nparts - q0);
+#pragma unroll 4
+    for (int j = 0; j < n; ++j) {
+      const float wj = readlane_f(w, j);
+      const float* po = a.part_o + ((base + q0 + j) * G + g) * D + lane * EPL;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] = fmaf(wj, po[e], acc[e]);
     }
-    out[d] = f32_to_bf16(acc * inv);
   }
-  if (a.lse && threadIdx.x == 0)
-    a.lse[int64_t(b) * Hq + hq] = (mm + fast_log2(S)) * kLn2;
+  S = wave_sum(S);
+  const float inv = 1.f / S;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) out[lane * EPL + e] = f32_to_bf16(acc[e] * inv);
+  if (a.lse && lane == 0) a.lse[int64_t(b) * Hq + hq] = (mx + fast_log2(S)) * kLn2;
 }
 
 template <int G, int D>
 void launch_partition(const DecodeArgs& a, int batch, hipStream_t s) {
-  const dim3 grid(unsigned(a.max_parts), unsigned(a.num_kv_heads), unsigned(batch));
-  decode_partition_kernel<G, D><<<grid, kThreads, 0, s>>>(a);
+  const dim3 grid(unsigned(a.num_kv_heads), unsigned(a.max_parts), unsigned(batch));
+  if constexpr (D == 128)
+    decode_lds_kernel<G><<<grid, kThreads, 0, s>>>(a);
+  else
+    decode_reg_kernel<G, D><<<grid, kThreads, 0, s>>>(a);
 }
 
 template <int D>
@@ -450,7 +738,7 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, int32_t batch,
 
   int ppp;
   if (pages_per_partition_hint > 0) {
-    ppp = (pages_per_partition_hint + 3) / 4 * 4;
+    ppp = std::min((pages_per_partition_hint + 3) / 4 * 4, kMaxPagesPerPart);
   } else {
     // Aim for ~8 workgroups per CU over (page, KV head) work, in multiples of
     // 4 pages (one per wave), between 8 and 128 pages per partition.
@@ -492,6 +780,7 @@ extern "C" int kvc_batch_decode_run(
   const int group = Hq / Hkv;
   KVC_REQUIRE(sched->page_size == kPage, KVC_ERR_UNSUPPORTED, "page_size must be 16");
   KVC_REQUIRE(sched->pages_per_partition > 0 && sched->pages_per_partition % 4 == 0 &&
+                  sched->pages_per_partition <= kMaxPagesPerPart &&
                   sched->max_partitions >= 1 && sched->max_partitions <= 65535,
               KVC_ERR_INVALID_ARG, "schedule not produced by kvc_decode_plan");
   KVC_REQUIRE(num_blocks > 0 && num_indices >= 0, KVC_ERR_INVALID_ARG,
@@ -499,8 +788,11 @@ extern "C" int kvc_batch_decode_run(
   KVC_REQUIRE(cache_token_stride >= int64_t(Hkv) * D &&
                   cache_block_stride >= cache_token_stride * kPage,
               KVC_ERR_INVALID_ARG, "cache strides smaller than the block");
+  KVC_REQUIRE(cache_token_stride * kPage < (int64_t(1) << 31), KVC_ERR_INVALID_ARG,
+              "a cache block spans more than 2^31 elements");
   KVC_REQUIRE(q_batch_stride >= int64_t(Hq) * D && out_batch_stride >= int64_t(Hq) * D,
               KVC_ERR_INVALID_ARG, "q/out batch stride smaller than Hq*head_dim");
+  KVC_REQUIRE(sm_scale > 0.f, KVC_ERR_INVALID_ARG, "sm_scale must be positive");
   const int vec_bytes = D == 64 ? 8 : 16;
   KVC_REQUIRE(aligned(q, vec_bytes) && aligned(key_cache, vec_bytes) &&
                   aligned(value_cache, vec_bytes) &&

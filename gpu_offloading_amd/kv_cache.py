@@ -39,9 +39,12 @@ class SwapHandle:
     src_block_ids: torch.Tensor          # device int32, evicted ids (concatenated)
     host: torch.Tensor                   # pinned uint8 [layers, n, 2, block_bytes]
     out_event: torch.cuda.Event          # D2H complete
+    out_start: Optional[torch.cuda.Event] = None   # side stream reached the swap-out
     in_event: Optional[torch.cuda.Event] = None
+    in_start: Optional[torch.cuda.Event] = None
     dst_block_ids: Optional[torch.Tensor] = None
     restored: bool = False
+    num_bytes: int = 0                   # bytes over the host link each way
     _keepalive: list = field(default_factory=list)
 
     @property
@@ -50,7 +53,17 @@ class SwapHandle:
 
     @property
     def bytes_per_direction(self) -> int:
-        return int(self.host.numel())
+        """Bytes that cross the host link each way (all layers, K and V)."""
+        return self.num_bytes
+
+    def out_seconds(self) -> float:
+        """Side-stream time of the swap-out (gathers + D2H copies); call after
+        ``out_event`` completed."""
+        return self.out_start.elapsed_time(self.out_event) * 1e-3
+
+    def in_seconds(self) -> float:
+        """Side-stream time of the swap-in (H2D copies + scatters)."""
+        return self.in_start.elapsed_time(self.in_event) * 1e-3
 
 
 class PagedKVCache:
@@ -385,13 +398,16 @@ class PagedKVCache:
         if self._dynamic_pages:
             self._reclaim(need=self.total_pages + 1)
 
-    def swap_out(self, seq_ids: Sequence[int]) -> SwapHandle:
+    def swap_out(self, seq_ids: Sequence[int], host: Optional[torch.Tensor] = None) -> SwapHandle:
         """Evict whole sequences to pinned host memory on the side stream.
 
         The sequences stop being resident (pages detached, block-table rows
         -1, length 0); their pages rejoin the free list once the copy is done.
         The side stream first waits for all work already enqueued on the
-        current stream, so earlier appends are included."""
+        current stream, so earlier appends are included.  ``host`` may be a
+        caller-allocated pinned uint8 buffer of at least
+        ``layers * pages * 2 * block_bytes`` bytes (otherwise one is
+        allocated)."""
         self._require_gpu()
         self._require_dynamic()
         seq_ids = [int(s) for s in seq_ids]
@@ -409,18 +425,24 @@ class PagedKVCache:
         self._lens_to_device()
         n = len(ids)
         bb = ops.block_bytes(self.k_cache[0])
-        host = torch.empty(self.num_layers * n * 2 * bb, dtype=torch.uint8, pin_memory=True)
+        nbytes = self.num_layers * n * 2 * bb
+        if host is None:
+            host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+        elif host.is_cuda or not host.is_pinned() or host.numel() * host.element_size() < nbytes:
+            raise RuntimeError(f"host buffer must be pinned CPU memory of >= {nbytes} bytes")
         ids_t = self._to_device(np.asarray(ids, dtype=np.int32))
         side = self._side_stream()
         side.wait_stream(cur)
         staging = self._staging_buf()
+        start = torch.cuda.Event(enable_timing=True)
+        start.record(side)
         ops.swap_out_blocks(self.k_cache, self.v_cache, ids_t, host, staging, stream=side)
         ids_t.record_stream(side)
-        ev = torch.cuda.Event()
+        ev = torch.cuda.Event(enable_timing=True)
         ev.record(side)
         # The host buffer must outlive the D2H copy even if the handle is dropped.
         self._pending_free.append((ev, ids, [ids_t, host]))
-        return SwapHandle(seq_ids, lens, npages, ids_t, host, ev)
+        return SwapHandle(seq_ids, lens, npages, ids_t, host, ev, out_start=start, num_bytes=nbytes)
 
     def swap_in(self, handle: SwapHandle, wait: bool = False) -> None:
         """Restore an evicted handle into freshly allocated pages.
@@ -447,11 +469,14 @@ class PagedKVCache:
         side = self._side_stream()
         side.wait_stream(cur)
         side.wait_event(handle.out_event)
+        start = torch.cuda.Event(enable_timing=True)
+        start.record(side)
         ops.swap_in_blocks(handle.host, dst_t, self.k_cache, self.v_cache, self._staging_buf(),
                            stream=side)
         dst_t.record_stream(side)
-        ev = torch.cuda.Event()
+        ev = torch.cuda.Event(enable_timing=True)
         ev.record(side)
+        handle.in_start = start
         self._pending_free.append((ev, [], [dst_t, handle.host]))
         handle.in_event = ev
         handle.dst_block_ids = dst_t

@@ -1,0 +1,301 @@
+"""Pins of the CPU oracle (oracle/kv_oracle.py), CPU only.
+
+The reference holds no golden vectors, known-answer tests or fixtures for this
+path (its arithmetic lives in vLLM 0.17.1 / FlashInfer, absent here), so each
+oracle function is pinned by checks that do not retype its formula:
+  bf16 conversion     torch's own float32 <-> bfloat16 casts (RNE)
+  page pool           the reference allocator's documented FIFO order and
+                      errors (moe_engine.py:4231-4297), worked by hand
+  slot mapping        identity block tables (static mode, moe_engine.py:504-519)
+                      give slot = seq * pages * 16 + pos; injectivity
+  plan                hand-worked indptr / last_page_len including len % 16 == 0
+  append / gather     element-by-element Python loops; append -> gather identity
+  decode attention    torch scaled_dot_product_attention (fp32, enable_gqa) and
+                      special cases: one token -> V[0], constant K -> mean(V)
+  merge               attention over A ++ B == merge(attn(A), attn(B))
+  block gather/scat.  byte images of the blocks; round-trip identity
+A deliberately planted mistake in each oracle function fails one of these
+(tests at the end plant them in copies of the oracle functions).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as orc
+
+
+def rand_bf16(rng, shape, std=1.0):
+    return orc.f32_to_bf16((rng.standard_normal(shape) * std).astype(np.float32))
+
+
+# ----------------------------------------------------------------- bf16
+def test_bf16_conversions_match_torch():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(10000).astype(np.float32) * 1e3,
+                        np.array([0.0, -0.0, 1.0, np.inf, -np.inf, 3.0e38, 1e-40,
+                                  1.00390625, 1.01171875], np.float32)])
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(orc.f32_to_bf16(x), ref)
+    back = torch.from_numpy(ref.view(np.int16)).view(torch.bfloat16).float().numpy()
+    assert np.array_equal(orc.bf16_to_f32(ref), back)
+    nan = orc.f32_to_bf16(np.array([np.nan], np.float32))
+    assert np.isnan(orc.bf16_to_f32(nan)).all()
+
+
+# ------------------------------------------------------------ page pool
+def test_fifo_pool_order_and_errors_by_hand():
+    pool = orc.FifoPagePool(6, 3, 4)
+    pool.alloc_pages(0, 2)                  # takes 0, 1
+    pool.alloc_pages(1, 3)                  # takes 2, 3, 4
+    assert pool.block_table[0].tolist() == [0, 1, -1, -1]
+    assert pool.block_table[1].tolist() == [2, 3, 4, -1]
+    pool.free_seq(0)                        # free list: 5, 0, 1
+    assert pool.block_table[0].tolist() == [-1] * 4
+    pool.alloc_pages(2, 2)                  # takes 5, 0
+    assert pool.block_table[2].tolist() == [5, 0, -1, -1]
+    assert (pool.pages_free, pool.pages_in_use) == (1, 5)
+    pool.alloc_pages(2, 0)                  # no-op
+    pool.alloc_pages(2, -3)                 # no-op
+    with pytest.raises(RuntimeError, match="only 1 free pages remain"):
+        pool.alloc_pages(0, 2)
+    with pytest.raises(RuntimeError, match="max_pages_per_seq"):
+        pool.alloc_pages(1, 2)
+    pool.ensure_pages(1, 2)                 # already has 3: no-op
+    pool.ensure_pages(0, 1)                 # takes 1
+    assert pool.block_table[0, 0] == 1 and pool.pages_free == 0
+    pool.reset()
+    assert pool.pages_free == 6 and (pool.block_table == -1).all()
+
+
+def test_fifo_pool_custom_free_order():
+    pool = orc.FifoPagePool(8, 2, 8, free_order=[7, 2, 5])
+    pool.alloc_pages(0, 2)
+    assert pool.block_table[0, :2].tolist() == [7, 2]
+    assert pool.pages_in_use == 7
+
+
+# --------------------------------------------------------- slot mapping
+def test_slot_mapping_identity_table_closed_form():
+    max_seqs, pages = 5, 7
+    bt = np.arange(max_seqs * pages, dtype=np.int32).reshape(max_seqs, pages)
+    rng = np.random.default_rng(1)
+    seqs = rng.integers(0, max_seqs, 200)
+    pos = rng.integers(0, pages * 16, 200)
+    got = orc.slot_mapping(bt, seqs, pos)
+    assert got.dtype == np.int64
+    assert np.array_equal(got, seqs * pages * 16 + pos)
+
+
+def test_slot_mapping_permuted_table_is_injective_and_consistent():
+    rng = np.random.default_rng(2)
+    bt = rng.permutation(4 * 9).astype(np.int32).reshape(4, 9)
+    seqs = np.repeat(np.arange(4), 9 * 16)
+    pos = np.tile(np.arange(9 * 16), 4)
+    s = orc.slot_mapping(bt, seqs, pos)
+    assert len(np.unique(s)) == len(s) == 4 * 9 * 16
+    assert np.array_equal(s // 16, bt[seqs, pos // 16]) and np.array_equal(s % 16, pos % 16)
+
+
+def test_step_slot_mapping_pads_with_minus_one():
+    bt = np.arange(3 * 4, dtype=np.int32).reshape(3, 4)
+    computed = np.array([5, 0, 17], np.int32)
+    slots, pos = orc.step_slot_mapping(bt, [2, 0], [1, 3], computed, graph_n=8)
+    assert pos.tolist() == [17, 5, 6, 7, 0, 0, 0, 0]
+    assert slots.tolist() == [2 * 64 + 17, 5, 6, 7, -1, -1, -1, -1]
+
+
+# ----------------------------------------------------------------- plan
+def test_plan_decode_by_hand():
+    indptr, lpl = orc.plan_decode([1, 16, 17, 0, 32, 33])
+    assert indptr.tolist() == [0, 1, 2, 4, 4, 6, 9]
+    assert lpl.tolist() == [1, 16, 1, 0, 16, 1]
+
+
+def test_page_indices_by_hand():
+    bt = np.array([[9, 8, 7], [1, 2, 3], [4, 5, 6]], np.int32)
+    indptr = np.array([0, 2, 3, 6], np.int32)
+    assert orc.page_indices(bt, [2, 0, 1], indptr).tolist() == [4, 5, 9, 1, 2, 3]
+
+
+# --------------------------------------------------------- append/gather
+def _loop_append(key, value, kc, vc, slots):
+    nb, bs, h, d = kc.shape
+    for i, s in enumerate(slots):
+        if s < 0 or s >= nb * bs:
+            continue
+        for hh in range(h):
+            for dd in range(d):
+                kc[s // bs, s % bs, hh, dd] = key[i, hh, dd]
+                vc[s // bs, s % bs, hh, dd] = value[i, hh, dd]
+
+
+def test_append_matches_elementwise_loop():
+    rng = np.random.default_rng(3)
+    nb, h, d, n = 6, 2, 4, 40
+    k = rand_bf16(rng, (n + 3, h, d))
+    v = rand_bf16(rng, (n + 3, h, d))
+    slots = rng.permutation(nb * 16)[:n].astype(np.int64)
+    slots[[3, 17]] = -1
+    slots[20] = nb * 16 + 5          # out of range: skipped
+    kc0 = rand_bf16(rng, (nb, 16, h, d))
+    vc0 = rand_bf16(rng, (nb, 16, h, d))
+    ek, ev = kc0.copy(), vc0.copy()
+    _loop_append(k, v, ek, ev, slots)
+    gk, gv = kc0.copy(), vc0.copy()
+    orc.reshape_and_cache(k, v, gk, gv, slots)
+    assert np.array_equal(gk, ek) and np.array_equal(gv, ev)
+
+
+def test_append_then_gather_is_identity_with_offsets():
+    rng = np.random.default_rng(4)
+    lens = [37, 128, 255, 1]
+    pool = orc.FifoPagePool(64, 4, 16, free_order=rng.permutation(64).tolist())
+    for s, ln in enumerate(lens):
+        pool.ensure_pages(s, (ln + 15) // 16)
+    seqs = np.concatenate([[s] * ln for s, ln in enumerate(lens)])
+    pos = np.concatenate([np.arange(ln) for ln in lens])
+    slots = orc.slot_mapping(pool.block_table, seqs, pos)
+    k = rand_bf16(rng, (len(slots), 2, 8))
+    v = rand_bf16(rng, (len(slots), 2, 8))
+    kc = np.zeros((64, 16, 2, 8), np.uint16)
+    vc = np.zeros_like(kc)
+    orc.reshape_and_cache(k, v, kc, vc, slots)
+    gk, gv = orc.gather_kv(kc, vc, pool.block_table, lens)
+    assert np.array_equal(gk, k) and np.array_equal(gv, v)
+    starts = [3, 100, 0, 0]
+    sub = [ln - st for ln, st in zip(lens, starts)]
+    gk2, _ = orc.gather_kv(kc, vc, pool.block_table, sub, starts)
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    exp = np.concatenate([k[cu[b] + starts[b]:cu[b + 1]] for b in range(4)])
+    assert np.array_equal(gk2, exp)
+
+
+# ------------------------------------------------------------- decode
+def _sdpa(q_bits, kc, vc, bt, lens):
+    q = torch.from_numpy(orc.bf16_to_f32(q_bits))
+    K = torch.from_numpy(orc.bf16_to_f32(kc))
+    V = torch.from_numpy(orc.bf16_to_f32(vc))
+    outs = []
+    for b, ln in enumerate(lens):
+        pages = torch.from_numpy(bt[b, :(ln + 15) // 16].astype(np.int64))
+        Kb = K[pages].flatten(0, 1)[:ln].transpose(0, 1).contiguous()
+        Vb = V[pages].flatten(0, 1)[:ln].transpose(0, 1).contiguous()
+        o = torch.nn.functional.scaled_dot_product_attention(q[b][:, None], Kb, Vb, enable_gqa=True)
+        outs.append(o[:, 0])
+    return torch.stack(outs).numpy()
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 16, 64), (8, 2, 32)])
+def test_paged_decode_matches_torch_sdpa(hq, hkv, d):
+    rng = np.random.default_rng(5)
+    lens = [1, 15, 16, 17, 100, 300]
+    pool = orc.FifoPagePool(64, len(lens), 32, free_order=rng.permutation(64).tolist())
+    for s, ln in enumerate(lens):
+        pool.ensure_pages(s, (ln + 15) // 16)
+    kc = rand_bf16(rng, (64, 16, hkv, d))
+    vc = rand_bf16(rng, (64, 16, hkv, d))
+    q = rand_bf16(rng, (len(lens), hq, d), std=2.0)
+    indptr, lpl = orc.plan_decode(lens)
+    idx = orc.page_indices(pool.block_table, range(len(lens)), indptr)
+    out, lse = orc.paged_decode(q, kc, vc, indptr, idx, lpl)
+    ref = _sdpa(q, kc, vc, pool.block_table, lens)
+    assert np.abs(out - ref).max() < 2e-5
+    # lse against torch.logsumexp of the scaled logits, one request
+    b, ln = 4, lens[4]
+    K = orc.bf16_to_f32(kc)[pool.block_table[b, :(ln + 15) // 16]].reshape(-1, hkv, d)[:ln]
+    qf = orc.bf16_to_f32(q)[b]
+    g = hq // hkv
+    logits = np.stack([qf[h] @ K[:, h // g].T for h in range(hq)]) / np.sqrt(d)
+    assert np.allclose(lse[b], torch.logsumexp(torch.from_numpy(logits), -1).numpy(), atol=1e-5)
+
+
+def test_paged_decode_special_cases():
+    rng = np.random.default_rng(6)
+    kc = rand_bf16(rng, (4, 16, 2, 16))
+    vc = rand_bf16(rng, (4, 16, 2, 16))
+    q = rand_bf16(rng, (2, 4, 16))
+    # one-token context: the output is V[0] of the mapped kv head
+    out, lse = orc.paged_decode(q, kc, vc, np.array([0, 1, 2], np.int32),
+                                np.array([3, 1], np.int32), np.array([1, 1], np.int32))
+    for b, page in enumerate([3, 1]):
+        exp = orc.bf16_to_f32(vc[page, 0])[[0, 0, 1, 1]]
+        assert np.array_equal(out[b], exp)
+    # constant K: uniform weights, the output is the mean of V over the context
+    kc2 = np.full_like(kc, orc.f32_to_bf16(np.float32(0.5)))
+    out, lse = orc.paged_decode(q[:1], kc2, vc, np.array([0, 2], np.int32),
+                                np.array([2, 0], np.int32), np.array([5], np.int32))
+    V = orc.bf16_to_f32(vc[[2, 0]]).reshape(-1, 2, 16)[:21]
+    assert np.allclose(out[0], V.mean(0)[[0, 0, 1, 1]], atol=1e-6)
+    # empty request: zero output, lse -inf
+    out, lse = orc.paged_decode(q[:1], kc, vc, np.array([0, 0], np.int32), np.zeros(0, np.int32),
+                                np.array([0], np.int32))
+    assert (out == 0).all() and np.isneginf(lse).all()
+
+
+def test_merge_of_split_context_equals_whole():
+    rng = np.random.default_rng(7)
+    kc = rand_bf16(rng, (16, 16, 2, 32))
+    vc = rand_bf16(rng, (16, 16, 2, 32))
+    q = rand_bf16(rng, (1, 8, 32), std=3.0)
+    pages = rng.permutation(16)[:10].astype(np.int32)
+    whole, lw = orc.paged_decode(q, kc, vc, np.array([0, 10], np.int32), pages, np.array([7], np.int32))
+    o1, l1 = orc.paged_decode(q, kc, vc, np.array([0, 4], np.int32), pages[:4], np.array([16], np.int32))
+    o2, l2 = orc.paged_decode(q, kc, vc, np.array([0, 6], np.int32), pages[4:], np.array([7], np.int32))
+    m, lm = orc.merge_attention_states(o1, l1, o2, l2)
+    assert np.allclose(m, whole, atol=1e-5) and np.allclose(lm, lw, atol=1e-5)
+    # merging with an empty state (lse -inf) is the identity
+    m2, l2m = orc.merge_attention_states(o1, l1, np.zeros_like(o1), np.full_like(l1, -np.inf))
+    assert np.allclose(m2, o1) and np.allclose(l2m, l1)
+
+
+# -------------------------------------------------------------- blocks
+def test_gather_scatter_blocks_byte_images():
+    rng = np.random.default_rng(8)
+    kc = rand_bf16(rng, (10, 16, 2, 8))
+    vc = rand_bf16(rng, (10, 16, 2, 8))
+    ids = np.array([7, 2, 9], np.int32)
+    st = orc.gather_blocks(kc, vc, ids)
+    assert st.shape == (3, 2, 16 * 2 * 8 * 2) and st.dtype == np.uint8
+    for i, b in enumerate(ids):
+        assert st[i, 0].tobytes() == kc[b].tobytes() and st[i, 1].tobytes() == vc[b].tobytes()
+    k2, v2 = np.zeros_like(kc), np.zeros_like(vc)
+    orc.scatter_blocks(st, [0, 5, 1], k2, v2)
+    assert np.array_equal(k2[[0, 5, 1]], kc[ids]) and np.array_equal(v2[[0, 5, 1]], vc[ids])
+    assert (k2[[2, 3, 4, 6, 7, 8, 9]] == 0).all()
+
+
+# ----------------------------------------------- planted mistakes fail
+def test_planted_mistakes_are_caught():
+    """Copies of oracle functions with a typical slip (wrong GQA head map,
+    missing scale, off-by-one last page) disagree with the pins above."""
+    rng = np.random.default_rng(9)
+    lens = [20, 33]
+    pool = orc.FifoPagePool(16, 2, 8, free_order=rng.permutation(16).tolist())
+    for s, ln in enumerate(lens):
+        pool.ensure_pages(s, (ln + 15) // 16)
+    kc = rand_bf16(rng, (16, 16, 2, 16))
+    vc = rand_bf16(rng, (16, 16, 2, 16))
+    q = rand_bf16(rng, (2, 4, 16), std=2.0)
+    indptr, lpl = orc.plan_decode(lens)
+    idx = orc.page_indices(pool.block_table, [0, 1], indptr)
+    ref = _sdpa(q, kc, vc, pool.block_table, lens)
+
+    def bad_decode(headmap=None, scale=None, lpl_shift=0):
+        qf = orc.bf16_to_f32(q)
+        out = np.zeros_like(qf)
+        for b in range(2):
+            pages = idx[indptr[b]:indptr[b + 1]]
+            n = (len(pages) - 1) * 16 + int(lpl[b]) + lpl_shift
+            K = orc.bf16_to_f32(kc[pages].reshape(-1, 2, 16)[:n])
+            V = orc.bf16_to_f32(vc[pages].reshape(-1, 2, 16)[:n])
+            for h in range(4):
+                kh = headmap(h) if headmap else h // 2
+                s = K[:, kh] @ qf[b, h] * (scale if scale else 1 / 4.0)
+                p = np.exp(s - s.max())
+                out[b, h] = p @ V[:, kh] / p.sum()
+        return out
+
+    assert np.abs(bad_decode() - ref).max() < 2e-5                        # the correct form
+    assert np.abs(bad_decode(headmap=lambda h: h % 2) - ref).max() > 1e-2  # interleaved map
+    assert np.abs(bad_decode(scale=1.0) - ref).max() > 1e-2                # no 1/sqrt(d)
+    assert np.abs(bad_decode(lpl_shift=-1) - ref).max() > 1e-3             # drops last token
