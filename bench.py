@@ -15,7 +15,7 @@ before the timed region starts.
 ``value`` is the step's algorithmic HBM bytes (decode: every K/V row read once
 per KV head + q in + out + page ids; append: rows read + written + slots)
 divided by the wall time of the step, so host setup and launch gaps count
-against it.  ``roofline`` is the decode-attention launch alone (partition +
+against it.  ``roofline`` is the decode-attention launch alone (streaming +
 merge kernel, bracketed by HIP events on the stream they run on) against the
 8 TB/s HBM3E peak.  ``extra`` carries the other rows of the metric: chunked-
 prefill append and gather GB/s (configuration 3), long-context decode GB/s
@@ -23,15 +23,16 @@ prefill append and gather GB/s (configuration 3), long-context decode GB/s
 (configuration 5).  ``cpu_baseline`` times the numpy oracle on one layer of
 the same workload on the host cores.
 
-Other modes used by the profiles:
+Other modes used by the profiles (one kernel family each, few launches):
   --mode copy     a plain device copy of known size (FETCH/WRITE calibration)
+  --mode decode2  configuration 2 decode, one layer, 10 launches
   --mode decode4  configuration 4 decode only (32 launches)
+  --mode append3  configuration 3 append + gather, one layer, 10 launches each
 """
 from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -55,21 +56,14 @@ def parse_args():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip configurations 3-5")
-    p.add_argument("--mode", default="step", choices=["step", "copy", "decode4"])
+    p.add_argument("--mode", default="step",
+                   choices=["step", "copy", "decode2", "decode4", "append3"])
     return p.parse_args()
 
 
 # --------------------------------------------------------------- helpers
 def _events(torch):
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-
-
-def _fill_normal(t, std=1.0):
-    """In-place N(0, std^2) bf16 fill on the device (chunked, no fp32 copy)."""
-    flat = t.view(-1)
-    step = 1 << 28
-    for i in range(0, flat.numel(), step):
-        flat[i:i + step].normal_(0.0, std)
 
 
 def build_cfg2_cache(torch, seed, num_layers=None):
@@ -162,7 +156,7 @@ def run_step_bench(torch, args):
     sched = cache._decode_wrapper.schedule
     log(f"cfg2: {ms_per_step:.3f} ms/step, step {step_gbps:.1f} GB/s, decode launch "
         f"{avg_ms * 1e3:.1f} us = {achieved:.1f} GB/s ({achieved / HBM_PEAK_GBPS:.1%} of peak); "
-        f"ppp {sched.pages_per_partition}, parts {sched.max_partitions}")
+        f"segments {sched.num_segments}x{sched.num_head_groups}, max parts {sched.max_partitions}")
     # sanity: the outputs are finite
     assert all(torch.isfinite(o.float()).all().item() for o in outs[:2]), "non-finite decode output"
     res = {
@@ -170,9 +164,9 @@ def run_step_bench(torch, args):
         "value": step_gbps,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
-                     "kernel": "decode_partition_kernel<4,128> + decode_merge_kernel<128>",
+                     "kernel": "decode_lds_kernel<4> + decode_merge_kernel<128>",
                      "avg_launch_us": avg_ms * 1e3, "algorithmic_bytes_per_launch": avg_bytes,
-                     "pages_per_partition": sched.pages_per_partition,
+                     "segments": sched.num_segments, "head_groups": sched.num_head_groups,
                      "max_partitions": sched.max_partitions},
     }
     del cache, qs, ks, vs, outs
@@ -181,7 +175,32 @@ def run_step_bench(torch, args):
 
 
 # ----------------------------------------------------------- extras
-def run_cfg3(torch, seed, reps=10):
+def run_decode2(torch, seed, reps=10):
+    """Configuration 2 decode attention (len + 1 tokens), one layer."""
+    from gpu_offloading_amd import workloads
+
+    cfg = workloads.config2(seed=seed)
+    sh = cfg.shape
+    lens = [ln + 1 for ln in cfg.seq_lens]
+    kc, vc, q, w = build_paged(torch, lens, sh.num_kv_heads, sh.head_dim, seed + 3,
+                               hq=sh.num_qo_heads)
+    out = torch.empty_like(q)
+    w.run(q, (kc, vc), out=out)
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(reps):
+        w.run(q, (kc, vc), out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / reps
+    b = workloads.decode_bytes(lens, sh.num_qo_heads, sh.num_kv_heads, sh.head_dim)
+    log(f"cfg2 decode: {t * 1e6:.1f} us, {b / t / 1e9:.0f} GB/s, {b} algorithmic bytes")
+    print(json.dumps({"mode": "decode2", "us": t * 1e6, "bytes": b, "GBps": b / t / 1e9}),
+          flush=True)
+
+
+def run_cfg3(torch, seed, reps=10, layers=None):
     """Chunked-prefill append of 8 x 2048 tokens per layer into a pool whose
     free list is a random 40% of its blocks, then gather of every sequence."""
     from gpu_offloading_amd import ops, workloads
@@ -189,7 +208,7 @@ def run_cfg3(torch, seed, reps=10):
 
     cfg = workloads.config3(seed=seed)
     sh = cfg.shape
-    L = sh.num_layers
+    L = layers or sh.num_layers
     pool = PagePool(cfg.total_pages, 8, 2048 // 16, free_order=cfg.free_order)
     bt = torch.full((8, 128), -1, dtype=torch.int32)
     for s in range(8):
@@ -292,7 +311,7 @@ def run_cfg4(torch, seed, reps=32):
     t = e0.elapsed_time(e1) * 1e-3 / reps
     b = workloads.decode_bytes(cfg.seq_lens, sh.num_qo_heads, sh.num_kv_heads, sh.head_dim)
     res = {"decode_GBps": b / t / 1e9, "decode_us": t * 1e6, "frac_of_peak": b / t / 1e9 / HBM_PEAK_GBPS,
-           "pages_per_partition": w.schedule.pages_per_partition}
+           "segments": w.schedule.num_segments}
     log(f"cfg4: decode {res['decode_GBps']:.0f} GB/s ({t * 1e6:.1f} us, "
         f"{res['frac_of_peak']:.1%} of peak)")
     del kc, vc, q, w, out
@@ -482,8 +501,14 @@ def main():
     if args.mode == "copy":
         run_copy_calibration(torch)
         return
+    if args.mode == "decode2":
+        run_decode2(torch, args.seed)
+        return
     if args.mode == "decode4":
         run_cfg4(torch, args.seed)
+        return
+    if args.mode == "append3":
+        print(json.dumps({"mode": "append3", **run_cfg3(torch, args.seed, layers=1)}), flush=True)
         return
 
     res = run_step_bench(torch, args)

@@ -20,6 +20,7 @@ LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libkvc.so")
 
 KVC_OK = 0
+KVC_ERR_WORKSPACE = 4
 STATUS_NAMES = {
     0: "KVC_OK",
     1: "KVC_ERR_INVALID_ARG",
@@ -39,10 +40,16 @@ class KvcDecodeSchedule(ctypes.Structure):
         ("num_kv_heads", c_int32),
         ("head_dim", c_int32),
         ("page_size", c_int32),
-        ("pages_per_partition", c_int32),
+        ("num_segments", c_int32),
+        ("num_head_groups", c_int32),
+        ("num_pieces", c_int32),
+        ("pieces_offset", c_int32),
+        ("nparts_offset", c_int32),
         ("max_partitions", c_int32),
         ("total_pages", c_int32),
         ("num_empty", c_int32),
+        ("reserved", c_int32),
+        ("plan_ints", c_int64),
         ("workspace_bytes", c_int64),
     ]
 
@@ -64,12 +71,13 @@ SIGNATURES = {
         _P, _P, _I32P, c_int64, c_int32, _I32P, _I32P,
         c_int32, c_int32, c_int32, c_int32, c_int32, c_int64, c_int32,
         c_int64, c_int64, _P, _P, c_int64, _I32P, _P]),
+    "kvc_decode_plan_ints": (c_int64, [c_int32, c_int32]),
     "kvc_decode_plan": (c_int, [
         c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
-        POINTER(KvcDecodeSchedule)]),
+        POINTER(KvcDecodeSchedule), c_void_p, c_int64]),
     "kvc_decode_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32]),
     "kvc_batch_decode_run": (c_int, [
-        POINTER(KvcDecodeSchedule), _P, c_int64, _P, _P, c_int64, c_int64, c_int64,
+        POINTER(KvcDecodeSchedule), _I32P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64,
         _I32P, _I32P, c_int64, _I32P, c_float, _P, c_int64, _P, c_int64, _P, _P]),
     "kvc_merge_attention_states": (c_int, [
         _P, _P, _P, _P, c_int64, c_int32, _P, _P, _P]),

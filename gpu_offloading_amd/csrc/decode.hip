@@ -9,27 +9,31 @@
 // src/dense/offload_kv_attn.py:24-39 (done in base 2 here).
 //
 // Decode is a GEMV: every K/V byte feeds only `group` query heads, so the
-// kernels are HBM-bound and run on the VALU (no MFMA).  Work decomposition:
-//   * grid (num_kv_heads, max_partitions, batch), KV head fastest: the
-//     workgroups of the heads of one page range are dispatched together (to
-//     the eight XCDs in turn), so the 2 KB token rows of a page are read by
-//     concurrent workgroups, and every XCD receives the same share of work
-//     whatever the spread of request lengths;
-//   * a 256-thread workgroup owns one (request, KV head, partition of
-//     pages_per_partition pages) and serves all `group` query heads of that KV
-//     head, so K/V are read from HBM exactly once; wave w takes pages
-//     p0 + w, p0 + w + 4, ...  Each wave's page ids are loaded once, one per
-//     lane, and broadcast with v_readlane, so no dependent global load sits
-//     in the streaming loop;
-//   * epilogue: the four waves merge through LDS; a request with one partition
-//     is written as bf16 directly, otherwise an fp32 partial + log2-sum-exp
-//     goes to the workspace and decode_merge_kernel folds them.
+// kernels are HBM-bound and run on the VALU (no MFMA).
+//
+// Schedule (balanced split-KV, computed on the host by kvc_decode_plan like
+// FlashInfer's plan()): the flattened page list indices[0 .. P) of the whole
+// batch is cut into S segments of equal length, S ~ the number of workgroups
+// the GPU holds at once, so every workgroup streams the same number of pages
+// and all finish together whatever the spread of request lengths.  A segment
+// crosses request boundaries; the part of a request inside one segment is a
+// "piece".  A request covered by one piece is written straight to the output;
+// otherwise each piece leaves an fp32 partial + log2-sum-exp in the workspace
+// and decode_merge_kernel folds them.
+//
+// Grid (S, ceil(Hkv / 4)), 256 threads: wave w of workgroup (s, y) owns KV
+// head 4y + w of segment s and serves all `group` query heads of that KV head,
+// so K/V are read from HBM exactly once.  The four waves of a workgroup read
+// four neighbouring heads of the same pages (1 KB contiguous per token row).
+// Waves are independent: no workgroup barrier.  A wave's page ids are loaded
+// once, one per lane (4 registers: up to 256 pages), and broadcast with
+// v_readlane, so no dependent global load sits in the streaming loop.
 //
 // head_dim 128 (the reference models) uses decode_lds_kernel: each wave stages
 // one page (16 tokens x 256 B of K and of V) from HBM through registers into
-// its own 8 KB LDS tile while the previous page is being consumed.  The tile
-// is stored with the 16-byte chunk c of token t at slot c ^ t, which makes
-// both read patterns below free of LDS bank conflicts:
+// its own LDS tile; the next two pages are in flight in two register stages
+// while a page is consumed.  Tile rows are padded to 272 B, which keeps both
+// read patterns below free of LDS bank conflicts:
 //   q.k : lane (token t, query head g) computes the whole 128-dim dot product
 //         with v_dot2_f32_bf16 from 16 ds_read_b128 of row t (the four lanes
 //         of a token read the same address); no cross-lane reduction;
@@ -48,12 +52,17 @@ namespace kvc {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
-constexpr int kPage = 16;      // tokens per page (the engine's page_size)
-constexpr int kTokPerRow = 4;  // register kernel: tokens of a page per 16-lane row
-constexpr int kMaxPagesPerPart = 4 * 64;  // a wave holds its page ids in 64 lanes
+constexpr int kWaves = kThreads / 64;  // KV heads per workgroup
+constexpr int kPage = 16;              // tokens per page (the engine's page_size)
+constexpr int kTokPerRow = 4;          // register kernel: tokens of a page per 16-lane row
+constexpr int kIdRegs = 4;             // page-id registers per lane
+constexpr int kMaxSegPages = 64 * kIdRegs;
+constexpr int kReadGroup = 4;  // LDS reads scheduled together
+constexpr int kStages = 2;  // pages in flight per wave (LDS kernel)
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kLog2e = 1.44269504088896340736f;
+
+inline int64_t align4(int64_t n) { return (n + 3) / 4 * 4; }
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -67,9 +76,10 @@ struct DecodeArgs {
   const int32_t* indices;
   int64_t num_indices;
   const int32_t* last_page_len;
+  const int32_t* seg_ptr;  // [S + 1]: pieces of segment s are [seg_ptr[s], seg_ptr[s+1])
+  const int4* pieces;      // (request, first slot, end slot, partial index or -1)
   float scale_log2;        // sm_scale * log2(e)
   int32_t num_kv_heads;
-  int32_t pages_per_part;
   int32_t max_parts;
   float* part_o;           // [batch][Hkv][max_parts][G][D]
   float* part_lse;         // [batch][Hkv][max_parts][G]   (log2 domain)
@@ -98,49 +108,73 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// Page ids of the calling wave: lane j holds the block id of the wave's j-th
-// page (page p0 + wave + 4j of the request), -1 past the end.
-__device__ __forceinline__ int32_t load_wave_page_ids(const DecodeArgs& a, int pbeg,
-                                                      int first, int nw, int lane) {
-  int32_t id = -1;
-  if (lane < nw) {
-    const int64_t slot = int64_t(pbeg) + first + int64_t(kWaves) * lane;
-    id = slot < a.num_indices ? a.indices[slot] : -1;
-  }
-  return id;
-}
+// Page ids of a segment: lane l of register r holds indices[g0 + l + 64 r].
+struct SegmentIds {
+  int32_t r[kIdRegs];
 
-// Wave-merge + output.  s_acc [kWaves][G][D], s_m / s_l [kWaves][G] hold each
-// wave's unnormalised accumulator and base-2 softmax statistics.
-template <int G, int D>
-__device__ __forceinline__ void finish_partition(const DecodeArgs& a, int b, int h, int part,
-                                                 int nparts, const float* s_acc,
-                                                 const float* s_m, const float* s_l) {
-  const int hq0 = h * G;
-  const int64_t part_base = (int64_t(b) * a.num_kv_heads + h) * a.max_parts + part;
-  for (int o = threadIdx.x; o < G * D; o += kThreads) {
-    const int g = o / D;
-    const int d = o - g * D;
-    float mm = kNegBig;
+  __device__ __forceinline__ void load(const DecodeArgs& a, int g0, int n, int lane) {
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, s_m[w * G + g]);
-    float L = 0.f, A = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float f = fast_exp2(s_m[w * G + g] - mm);
-      L = fmaf(s_l[w * G + g], f, L);
-      A = fmaf(s_acc[(w * G + g) * D + d], f, A);
+    for (int i = 0; i < kIdRegs; ++i) {
+      const int j = lane + 64 * i;
+      const int64_t slot = int64_t(g0) + j;
+      r[i] = (j < n && slot < a.num_indices) ? a.indices[slot] : -1;
     }
-    const float res = L > 0.f ? A / L : 0.f;
-    const float lse2 = L > 0.f ? mm + fast_log2(L) : -INFINITY;
-    if (nparts == 1) {
-      a.out[int64_t(b) * a.out_stride + int64_t(hq0 + g) * D + d] = f32_to_bf16(res);
-      if (a.lse && d == 0)
-        a.lse[int64_t(b) * a.num_kv_heads * G + hq0 + g] = lse2 * kLn2;
+  }
+  // Block id of the segment's j-th page (j uniform).
+  __device__ __forceinline__ int32_t at(int j) const {
+    const int w = j >> 6;
+    int32_t v = r[0];
+#pragma unroll
+    for (int i = 1; i < kIdRegs; ++i) v = w == i ? r[i] : v;
+    return __builtin_amdgcn_readlane(v, j & 63);
+  }
+};
+
+// The piece being streamed by a wave and what the page loop needs of it.
+struct Piece {
+  int4 desc;     // (request, first slot, end slot, partial index or -1)
+  int req_last;  // slot of the request's final page
+  int last_len;  // tokens in that page
+
+  __device__ __forceinline__ void load(const DecodeArgs& a, int k) {
+    desc = a.pieces[k];
+    req_last = a.indptr[desc.x + 1] - 1;
+    last_len = min(max(a.last_page_len[desc.x], 0), kPage);
+  }
+  __device__ __forceinline__ int valid(int slot, int32_t blk, int64_t num_blocks) const {
+    if (blk < 0 || blk >= num_blocks) return 0;
+    return slot == req_last ? last_len : kPage;
+  }
+};
+
+// Output of a finished piece for query head hq = h * group + g: the final
+// bf16 row (a request covered by one piece) or an fp32 partial; `o` holds
+// this lane's NDIM normalised values starting at dim d0.
+template <int D, int NDIM>
+__device__ __forceinline__ void write_piece(const DecodeArgs& a, const int4& pc, int h,
+                                            int group, int g, int d0, const float (&o)[NDIM],
+                                            float lse2, bool lse_lane) {
+  const int b = pc.x;
+  const int hq = h * group + g;
+  if (pc.w < 0) {
+    uint16_t* dst = a.out + int64_t(b) * a.out_stride + int64_t(hq) * D + d0;
+    if constexpr (NDIM % 2 == 0) {
+#pragma unroll
+      for (int e = 0; e < NDIM; e += 2)
+        *reinterpret_cast<uint32_t*>(dst + e) =
+            uint32_t(f32_to_bf16(o[e])) | (uint32_t(f32_to_bf16(o[e + 1])) << 16);
     } else {
-      a.part_o[(part_base * G + g) * D + d] = res;
-      if (d == 0) a.part_lse[part_base * G + g] = lse2;
+#pragma unroll
+      for (int e = 0; e < NDIM; ++e) dst[e] = f32_to_bf16(o[e]);
     }
+    if (a.lse && lse_lane)
+      a.lse[int64_t(b) * a.num_kv_heads * group + hq] = lse2 * kLn2;
+  } else {
+    const int64_t pr = ((int64_t(b) * a.num_kv_heads + h) * a.max_parts + pc.w) * group + g;
+    float* dst = a.part_o + pr * D + d0;
+#pragma unroll
+    for (int e = 0; e < NDIM; ++e) dst[e] = o[e];
+    if (lse_lane) a.part_lse[pr] = lse2;
   }
 }
 
@@ -155,10 +189,15 @@ struct LdsCfg {
   static constexpr int CH = 16 / NS;            // 16-byte chunks of a K row per lane
 };
 
+// One wave's LDS tile: K and V of one page of one KV head, 16 token rows of
+// 256 B each stored with a 16 B pad (272 B row pitch), so that the 16 rows
+// read by one instruction start on 16 different 4-bank groups, and every
+// lane address is a per-lane base plus an immediate offset.
+constexpr int kRowPitch = 17;  // uint4 per padded row
 struct __align__(16) PageTile {
-  uint4 k[kPage * 16];  // [token][slot], slot = chunk ^ token
-  uint4 v[kPage * 16];
-  float p[kPage * 8];   // softmax weights p[token][query head], G <= 8
+  uint4 k[kPage * kRowPitch];
+  uint4 v[kPage * kRowPitch];
+  float p[kPage * 8];  // softmax weights p[token][query head], G <= 8
 };
 
 template <int G>
@@ -166,113 +205,117 @@ __global__ __launch_bounds__(kThreads) void decode_lds_kernel(DecodeArgs a) {
   using C = LdsCfg<G>;
   constexpr int D = 128;
   __shared__ PageTile s_tile[kWaves];
-  static_assert(sizeof(s_tile) >= sizeof(float) * (kWaves * G * D + 2 * kWaves * G),
-                "epilogue does not fit in the page tiles");
 
-  const int h = blockIdx.x;
-  const int part = blockIdx.y;
-  const int b = blockIdx.z;
-  const int pbeg = a.indptr[b];
-  const int npages = a.indptr[b + 1] - pbeg;
-  const int p0 = part * a.pages_per_part;
-  if (p0 >= npages) return;  // uniform over the workgroup
-  const int p1 = min(p0 + a.pages_per_part, npages);
-  const int nparts = (npages + a.pages_per_part - 1) / a.pages_per_part;
-  const int last_len = min(max(a.last_page_len[b], 0), kPage);
-
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
+  const int seg = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.y * kWaves + wave;
+  if (h >= a.num_kv_heads) return;  // whole wave; the kernel has no barrier
+  int k = a.seg_ptr[seg];
+  const int k_end = a.seg_ptr[seg + 1];
+  if (k >= k_end) return;
   PageTile& tile = s_tile[wave];
+  const int g0 = a.pieces[k].y;
+  const int n = min(a.pieces[k_end - 1].z - g0, kMaxSegPages);
 
   // q.k role: token t, query head gq (and gq + 4 when G == 8), dim split.
   const int t = lane & 15;
   const int row = lane >> 4;
   const int gq = row % C::GP;
   const int split = row / C::GP;
-  uint32_t qw[C::QL][C::CH * 4];
-#pragma unroll
-  for (int ql = 0; ql < C::QL; ++ql) {
-    const uint4* qp = reinterpret_cast<const uint4*>(
-        a.q + int64_t(b) * a.q_stride + int64_t(h * G + gq + 4 * ql) * D + split * C::CH * 8);
-#pragma unroll
-    for (int i = 0; i < C::CH; ++i) {
-      const uint4 x = qp[i];
-      qw[ql][4 * i + 0] = x.x;
-      qw[ql][4 * i + 1] = x.y;
-      qw[ql][4 * i + 2] = x.z;
-      qw[ql][4 * i + 3] = x.w;
-    }
-  }
-  // Staging role: load instruction u moves tokens 4u..4u+3; lane -> (token, slot).
+  // Staging role: load u moves tokens 4u..4u+3; lane -> (token 4u + lane/16,
+  // 16-byte chunk lane%16) of this KV head.
   const int st_tok = lane >> 4;
-  const int st_slot = lane & 15;
-  int32_t st_off[4];
+  const uint32_t st_goff = uint32_t(st_tok) * uint32_t(a.token_stride * 2) +
+                           uint32_t(h * D * 2) + uint32_t((lane & 15) * 16);
+  const uint32_t st_gstep = uint32_t(4 * a.token_stride * 2);  // bytes per load u
+  const int st_loff = st_tok * kRowPitch + (lane & 15);         // uint4 index in tile
+  const char* kbytes = reinterpret_cast<const char*>(a.k_cache);
+  const char* vbytes = reinterpret_cast<const char*>(a.v_cache);
+  const int64_t block_bytes = a.block_stride * 2;
+
+  SegmentIds ids;
+  ids.load(a, g0, n, lane);
+  Piece pc;
+  pc.load(a, k);
+
+  uint32_t qw[C::QL][C::CH * 4];
+  auto load_q = [&](int b) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int tok = 4 * u + st_tok;
-    st_off[u] = int32_t(tok * a.token_stride) + h * D + ((st_slot ^ tok) << 3);
-  }
-  // p.v role: dims 2*lane, 2*lane+1 = word lane&3 of chunk lane>>2.
-  const int vchunk = lane >> 2;
-  const int vword = lane & 3;
-
-  const int nw = p1 - p0 > wave ? (p1 - p0 - wave + kWaves - 1) / kWaves : 0;
-  const int32_t my_ids = load_wave_page_ids(a, pbeg, p0 + wave, nw, lane);
-
+    for (int ql = 0; ql < C::QL; ++ql) {
+      const uint4* qp = reinterpret_cast<const uint4*>(
+          a.q + int64_t(b) * a.q_stride + int64_t(h * G + gq + 4 * ql) * D + split * C::CH * 8);
+#pragma unroll
+      for (int i = 0; i < C::CH; ++i) {
+        const uint4 x = qp[i];
+        qw[ql][4 * i + 0] = x.x;
+        qw[ql][4 * i + 1] = x.y;
+        qw[ql][4 * i + 2] = x.z;
+        qw[ql][4 * i + 3] = x.w;
+      }
+    }
+  };
   float m_run[C::QL], l_run[C::QL], acc[G][2];
+  auto reset = [&]() {
 #pragma unroll
-  for (int ql = 0; ql < C::QL; ++ql) {
-    m_run[ql] = kNegBig;
-    l_run[ql] = 0.f;
-  }
+    for (int ql = 0; ql < C::QL; ++ql) {
+      m_run[ql] = kNegBig;
+      l_run[ql] = 0.f;
+    }
 #pragma unroll
-  for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
+    for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
+  };
+  auto finalize = [&]() {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float l = readlane_f(l_run[g / 4], 16 * (g % 4));
+      const float m = readlane_f(m_run[g / 4], 16 * (g % 4));
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      const float o[2] = {acc[g][0] * inv, acc[g][1] * inv};
+      write_piece<D, 2>(a, pc.desc, h, G, g, 2 * lane, o,
+                        l > 0.f ? m + fast_log2(l) : -INFINITY, lane == 0);
+    }
+  };
 
-  uint4 rk[4], rv[4];
-  auto issue = [&](int32_t blk) {
-    const int64_t base = int64_t(blk) * a.block_stride;
+  // A ring of kStages register stages: while page j is consumed from the LDS
+  // tile, pages j+1 .. j+kStages are in flight (kStages x 8 KB per wave).
+  struct Stage {
+    uint4 k[4], v[4];
+  };
+  auto issue = [&](Stage& r, int32_t blk) {
+    // Uniform block base (SGPRs) + 32-bit lane offset.
+    const char* kb = kbytes + int64_t(blk) * block_bytes;
+    const char* vb = vbytes + int64_t(blk) * block_bytes;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      rk[u] = *reinterpret_cast<const uint4*>(a.k_cache + base + st_off[u]);
-      rv[u] = *reinterpret_cast<const uint4*>(a.v_cache + base + st_off[u]);
+      r.k[u] = *reinterpret_cast<const uint4*>(kb + u * st_gstep + st_goff);
+      r.v[u] = *reinterpret_cast<const uint4*>(vb + u * st_gstep + st_goff);
     }
   };
   auto safe_id = [&](int32_t id) { return (id >= 0 && id < a.num_blocks) ? id : 0; };
-
-  int32_t blk = nw > 0 ? __builtin_amdgcn_readlane(my_ids, 0) : 0;
-  if (nw > 0) issue(safe_id(blk));
-  for (int j = 0; j < nw; ++j) {
-    const int pi = p0 + wave + kWaves * j;
-    const bool blk_ok = blk >= 0 && blk < a.num_blocks;
-    const int valid = !blk_ok ? 0 : (pi == npages - 1 ? last_len : kPage);
+  auto stage_tile = [&](Stage& r, int valid) {
     if (valid < kPage) {
       // Rows past the end may hold anything (even NaN bits): stage zeros so
       // that 0 * v stays 0.
 #pragma unroll
       for (int u = 0; u < 4; ++u)
-        if (4 * u + st_tok >= valid) rk[u] = rv[u] = make_uint4(0, 0, 0, 0);
+        if (4 * u + st_tok >= valid) r.k[u] = r.v[u] = make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      tile.k[u * 64 + lane] = rk[u];
-      tile.v[u * 64 + lane] = rv[u];
+      tile.k[st_loff + u * 4 * kRowPitch] = r.k[u];
+      tile.v[st_loff + u * 4 * kRowPitch] = r.v[u];
     }
-    if (j + 1 < nw) {
-      blk = __builtin_amdgcn_readlane(my_ids, j + 1);
-      issue(safe_id(blk));  // in flight while this page is consumed
-    }
-    wave_lds_fence();
-
+  };
+  auto consume = [&](int valid) {
     // q.k: lane (t, gq) over its chunks of K row t.
     float dots[C::QL];
 #pragma unroll
     for (int ql = 0; ql < C::QL; ++ql) dots[ql] = 0.f;
-    const uint4* krow = tile.k + t * 16;
+    const uint4* krow = tile.k + t * kRowPitch + split * C::CH;
 #pragma unroll
     for (int i = 0; i < C::CH; ++i) {
-      const int c = split * C::CH + i;
-      const uint4 kv = krow[c ^ t];
+      const uint4 kv = krow[i];
 #pragma unroll
       for (int ql = 0; ql < C::QL; ++ql) {
         dots[ql] = dot2_bf16(qw[ql][4 * i + 0], kv.x, dots[ql]);
@@ -280,6 +323,9 @@ __global__ __launch_bounds__(kThreads) void decode_lds_kernel(DecodeArgs a) {
         dots[ql] = dot2_bf16(qw[ql][4 * i + 2], kv.z, dots[ql]);
         dots[ql] = dot2_bf16(qw[ql][4 * i + 3], kv.w, dots[ql]);
       }
+      // Keep a bounded number of LDS reads in flight: hoisting all of them
+      // would cost registers, and with them a wave per SIMD.
+      if ((i + 1) % kReadGroup == 0) __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int off = 16 * C::GP; off < 64; off <<= 1)
@@ -308,11 +354,10 @@ __global__ __launch_bounds__(kThreads) void decode_lds_kernel(DecodeArgs a) {
     wave_lds_fence();
 
     // p.v over the 16 tokens of the page (rows past `valid` are zero).
-    const char* vbase = reinterpret_cast<const char*>(tile.v) + vword * 4;
+    const uint32_t* vcol = reinterpret_cast<const uint32_t*>(tile.v) + lane;
 #pragma unroll
     for (int tt = 0; tt < kPage; ++tt) {
-      const uint32_t vw =
-          *reinterpret_cast<const uint32_t*>(vbase + tt * 256 + ((vchunk ^ tt) << 4));
+      const uint32_t vw = vcol[tt * kRowPitch * 4];
       const float v0 = bf16lo(vw);
       const float v1 = bf16hi(vw);
       float pg[G];
@@ -334,28 +379,46 @@ __global__ __launch_bounds__(kThreads) void decode_lds_kernel(DecodeArgs a) {
         acc[g][0] = fmaf(pg[g], v0, acc[g][0]);
         acc[g][1] = fmaf(pg[g], v1, acc[g][1]);
       }
+      if ((tt + 1) % kReadGroup == 0) __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Page j of the segment, held in stage r (block id `id`), then the refill
+  // of r with page j+kStages and, at the end of a piece, its output.
+  auto step = [&](int j, Stage& r, int32_t& id) {
+    const int slot = g0 + j;
+    const int valid = pc.valid(slot, id, a.num_blocks);
+    stage_tile(r, valid);
+    if (j + kStages < n) {
+      id = ids.at(j + kStages);
+      issue(r, safe_id(id));
     }
     wave_lds_fence();
-  }
-
-  // Workgroup epilogue (the page tiles are reused for the wave partials).
-  __syncthreads();
-  float* s_acc = reinterpret_cast<float*>(s_tile);
-  float* s_m = s_acc + kWaves * G * D;
-  float* s_l = s_m + kWaves * G;
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-    *reinterpret_cast<float2*>(s_acc + (wave * G + g) * D + 2 * lane) =
-        make_float2(acc[g][0], acc[g][1]);
-  if (t == 0 && row < C::GP) {
-#pragma unroll
-    for (int ql = 0; ql < C::QL; ++ql) {
-      s_m[wave * G + gq + 4 * ql] = m_run[ql];
-      s_l[wave * G + gq + 4 * ql] = l_run[ql];
+    consume(valid);
+    wave_lds_fence();
+    if (slot + 1 == pc.desc.z) {
+      finalize();
+      if (++k < k_end) {
+        pc.load(a, k);
+        load_q(pc.desc.x);
+        reset();
+      }
     }
+  };
+
+  load_q(pc.desc.x);
+  reset();
+  Stage ring[kStages];
+  int32_t ring_id[kStages];
+#pragma unroll
+  for (int r = 0; r < kStages; ++r) {
+    ring_id[r] = r < n ? ids.at(r) : 0;
+    if (r < n) issue(ring[r], safe_id(ring_id[r]));
   }
-  __syncthreads();
-  finish_partition<G, D>(a, b, h, part, nparts, s_acc, s_m, s_l);
+  for (int j0 = 0; j0 < n; j0 += kStages) {
+#pragma unroll
+    for (int r = 0; r < kStages; ++r)
+      if (j0 + r < n) step(j0 + r, ring[r], ring_id[r]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -456,103 +519,103 @@ template <int G, int D>
 __global__ __launch_bounds__(kThreads) void decode_reg_kernel(DecodeArgs a) {
   constexpr int W = D / 32;
   constexpr int E = D / 16;
-  __shared__ float s_acc[kWaves * G * D];
-  __shared__ float s_m[kWaves * G];
-  __shared__ float s_l[kWaves * G];
-  const int h = blockIdx.x;
-  const int part = blockIdx.y;
-  const int b = blockIdx.z;
-  const int pbeg = a.indptr[b];
-  const int npages = a.indptr[b + 1] - pbeg;
-  const int p0 = part * a.pages_per_part;
-  if (p0 >= npages) return;  // uniform over the workgroup
-  const int p1 = min(p0 + a.pages_per_part, npages);
-  const int nparts = (npages + a.pages_per_part - 1) / a.pages_per_part;
-  const int last_len = min(max(a.last_page_len[b], 0), kPage);
-
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
+  const int seg = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.y * kWaves + wave;
+  if (h >= a.num_kv_heads) return;
+  int k = a.seg_ptr[seg];
+  const int k_end = a.seg_ptr[seg + 1];
+  if (k >= k_end) return;
+  const int g0 = a.pieces[k].y;
+  const int n = min(a.pieces[k_end - 1].z - g0, kMaxSegPages);
   const int row = lane >> 4;
   const int col = lane & 15;
+  const int64_t lane_off = int64_t(row) * a.token_stride + int64_t(h) * D + col * E;
+
+  SegmentIds ids;
+  ids.load(a, g0, n, lane);
+  Piece pc;
+  pc.load(a, k);
 
   uint32_t qw[G][W];
-  const uint16_t* qb = a.q + int64_t(b) * a.q_stride + int64_t(h) * G * D + col * E;
+  auto load_q = [&](int b) {
+    const uint16_t* qb = a.q + int64_t(b) * a.q_stride + int64_t(h) * G * D + col * E;
 #pragma unroll
-  for (int g = 0; g < G; ++g) load_slice<D>(qw[g], qb + g * D);
-
+    for (int g = 0; g < G; ++g) load_slice<D>(qw[g], qb + g * D);
+  };
   float m[G], l[G], acc[G][E];
+  auto reset = [&]() {
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = kNegBig;
-    l[g] = 0.f;
+    for (int g = 0; g < G; ++g) {
+      m[g] = kNegBig;
+      l[g] = 0.f;
 #pragma unroll
-    for (int e = 0; e < E; ++e) acc[g][e] = 0.f;
-  }
-
-  const int64_t lane_off = int64_t(row) * a.token_stride + int64_t(h) * D + col * E;
-  const int nw = p1 - p0 > wave ? (p1 - p0 - wave + kWaves - 1) / kWaves : 0;
-  const int32_t my_ids = load_wave_page_ids(a, pbeg, p0 + wave, nw, lane);
-  auto id_at = [&](int j) { return __builtin_amdgcn_readlane(my_ids, j); };
-  auto safe = [&](int32_t id) { return (id >= 0 && id < a.num_blocks) ? id : 0; };
-  auto valid_at = [&](int j, int32_t id) {
-    if (id < 0 || id >= a.num_blocks) return 0;
-    return p0 + wave + kWaves * j == npages - 1 ? last_len : kPage;
+      for (int e = 0; e < E; ++e) acc[g][e] = 0.f;
+    }
+  };
+  auto finalize = [&]() {
+    // Merge the four rows (lanes c, c+16, c+32, c+48 hold the same dims).
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float mo = __shfl_xor(m[g], off);
+        const float lo = __shfl_xor(l[g], off);
+        const float mm = fmaxf(m[g], mo);
+        const float wa = fast_exp2(m[g] - mm);
+        const float wb = fast_exp2(mo - mm);
+        l[g] = l[g] * wa + lo * wb;
+        m[g] = mm;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const float ao = __shfl_xor(acc[g][e], off);
+          acc[g][e] = acc[g][e] * wa + ao * wb;
+        }
+      }
+    }
+    if (row == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
+        float o[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[e] = acc[g][e] * inv;
+        write_piece<D, E>(a, pc.desc, h, G, g, col * E, o,
+                          l[g] > 0.f ? m[g] + fast_log2(l[g]) : -INFINITY, col == 0);
+      }
+    }
   };
 
   // Two register sets: page j is consumed while page j+1 is in flight.
+  auto safe = [&](int32_t id) { return (id >= 0 && id < a.num_blocks) ? id : 0; };
   PageRegs<D> ra, rb;
-  int32_t ida = 0, idb = 0;
-  if (nw > 0) {
-    ida = id_at(0);
-    load_page_regs<D>(a, ra, safe(ida), lane_off);
-  }
-  for (int j = 0; j < nw; j += 2) {
-    if (j + 1 < nw) {
-      idb = id_at(j + 1);
-      load_page_regs<D>(a, rb, safe(idb), lane_off);
+  auto step = [&](int j, PageRegs<D>& cur, int32_t id, PageRegs<D>& nxt, int32_t& nid) {
+    const int slot = g0 + j;
+    if (j + 1 < n) {
+      nid = ids.at(j + 1);
+      load_page_regs<D>(a, nxt, safe(nid), lane_off);
     }
-    consume_page_regs<G, D>(qw, ra, valid_at(j, ida), row, a.scale_log2, m, l, acc);
-    if (j + 1 >= nw) break;
-    if (j + 2 < nw) {
-      ida = id_at(j + 2);
-      load_page_regs<D>(a, ra, safe(ida), lane_off);
+    consume_page_regs<G, D>(qw, cur, pc.valid(slot, id, a.num_blocks), row, a.scale_log2,
+                            m, l, acc);
+    if (slot + 1 == pc.desc.z) {
+      finalize();
+      if (++k < k_end) {
+        pc.load(a, k);
+        load_q(pc.desc.x);
+        reset();
+      }
     }
-    consume_page_regs<G, D>(qw, rb, valid_at(j + 1, idb), row, a.scale_log2, m, l, acc);
-  }
+  };
 
-  // Merge the four rows of the wave (lanes c, c+16, c+32, c+48 hold the same dims).
-#pragma unroll
-  for (int off = 16; off <= 32; off <<= 1) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float mo = __shfl_xor(m[g], off);
-      const float lo = __shfl_xor(l[g], off);
-      const float mm = fmaxf(m[g], mo);
-      const float wa = fast_exp2(m[g] - mm);
-      const float wb = fast_exp2(mo - mm);
-      l[g] = l[g] * wa + lo * wb;
-      m[g] = mm;
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const float ao = __shfl_xor(acc[g][e], off);
-        acc[g][e] = acc[g][e] * wa + ao * wb;
-      }
-    }
+  load_q(pc.desc.x);
+  reset();
+  int32_t ida = ids.at(0), idb = 0;
+  load_page_regs<D>(a, ra, safe(ida), lane_off);
+  for (int j = 0; j < n; j += 2) {
+    step(j, ra, ida, rb, idb);
+    if (j + 1 < n) step(j + 1, rb, idb, ra, ida);
   }
-  if (row == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int e = 0; e < E; ++e) s_acc[(wave * G + g) * D + col * E + e] = acc[g][e];
-      if (col == 0) {
-        s_m[wave * G + g] = m[g];
-        s_l[wave * G + g] = l[g];
-      }
-    }
-  }
-  __syncthreads();
-  finish_partition<G, D>(a, b, h, part, nparts, s_acc, s_m, s_l);
 }
 
 // ---------------------------------------------------------------------------
@@ -561,8 +624,7 @@ __global__ __launch_bounds__(kThreads) void decode_reg_kernel(DecodeArgs a) {
 struct MergeArgs {
   const float* part_o;
   const float* part_lse;
-  const int32_t* indptr;
-  int32_t pages_per_part;
+  const int32_t* req_nparts;
   int32_t max_parts;
   int32_t num_kv_heads;
   int32_t group;
@@ -585,9 +647,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // One wave per (request, query head): lane p reads the log2-sum-exp of
 // partition p, the wave forms the weights, then every lane folds its D/64
-// dims over the partitions (independent loads, unrolled).  Requests with a
-// single partition were finished by the partition kernel; requests with no
-// pages get a zero output and lse = -inf.
+// dims over the partitions.  Requests with a single piece were finished by
+// the streaming kernel; requests with no pages get a zero output and
+// lse = -inf.
 template <int D>
 __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
   constexpr int EPL = D / 64;  // dims per lane
@@ -595,9 +657,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
   const int b = blockIdx.y;
   const int lane = threadIdx.x;
   const int G = a.group;
-  const int npages = a.indptr[b + 1] - a.indptr[b];
-  const int nparts = min(max((npages + a.pages_per_part - 1) / a.pages_per_part, 0),
-                         a.max_parts);
+  const int nparts = min(a.req_nparts[b], a.max_parts);
   if (nparts == 1) return;
   uint16_t* out = a.out + int64_t(b) * a.out_stride + int64_t(hq) * D;
   const int Hq = a.num_kv_heads * G;
@@ -609,7 +669,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
   float mx = -INFINITY;
   for (int p = lane; p < nparts; p += 64) mx = fmaxf(mx, lp[int64_t(p) * G]);
   mx = wave_max(mx);
-  if (nparts == 0 || mx == -INFINITY) {
+  if (nparts <= 0 || mx == -INFINITY) {
 #pragma unroll
     for (int e = 0; e < EPL; ++e) out[lane * EPL + e] = 0;
     if (a.lse && lane == 0) a.lse[int64_t(b) * Hq + hq] = -INFINITY;
@@ -622,9 +682,8 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
   for (int q0 = 0; q0 < nparts; q0 += 64) {
     const float w = q0 + lane < nparts ? fast_exp2(lp[int64_t(q0 + lane) * G] - mx) : 0.f;
     S += w;
-    const int n = min(64, nparts - q0);
-#pragma unroll 4
-    for (int j = 0; j < n; ++j) {
+    const int cnt = min(64, nparts - q0);
+    for (int j = 0; j < cnt; ++j) {
       const float wj = readlane_f(w, j);
       const float* po = a.part_o + ((base + q0 + j) * G + g) * D + lane * EPL;
 #pragma unroll
@@ -639,8 +698,8 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
 }
 
 template <int G, int D>
-void launch_partition(const DecodeArgs& a, int batch, hipStream_t s) {
-  const dim3 grid(unsigned(a.num_kv_heads), unsigned(a.max_parts), unsigned(batch));
+void launch_segments(const DecodeArgs& a, int segments, int head_groups, hipStream_t s) {
+  const dim3 grid{unsigned(segments), unsigned(head_groups)};
   if constexpr (D == 128)
     decode_lds_kernel<G><<<grid, kThreads, 0, s>>>(a);
   else
@@ -648,14 +707,22 @@ void launch_partition(const DecodeArgs& a, int batch, hipStream_t s) {
 }
 
 template <int D>
-bool dispatch_group(int group, const DecodeArgs& a, int batch, hipStream_t s) {
+bool dispatch_group(int group, const DecodeArgs& a, int segments, int head_groups,
+                    hipStream_t s) {
   switch (group) {
-    case 1: launch_partition<1, D>(a, batch, s); return true;
-    case 2: launch_partition<2, D>(a, batch, s); return true;
-    case 4: launch_partition<4, D>(a, batch, s); return true;
-    case 8: launch_partition<8, D>(a, batch, s); return true;
+    case 1: launch_segments<1, D>(a, segments, head_groups, s); return true;
+    case 2: launch_segments<2, D>(a, segments, head_groups, s); return true;
+    case 4: launch_segments<4, D>(a, segments, head_groups, s); return true;
+    case 8: launch_segments<8, D>(a, segments, head_groups, s); return true;
     default: return false;
   }
+}
+
+// Workgroups of the streaming kernel one CU holds at once (register-limited;
+// from the compiled kernels' VGPR counts), used to size the schedule.
+int resident_workgroups_per_cu(int group, int head_dim) {
+  if (head_dim == 128) return group <= 2 ? 3 : (group == 4 ? 2 : 1);
+  return group <= 2 ? 2 : 1;
 }
 
 // Merge of two bf16 attention states (a8 as a standalone op).
@@ -703,11 +770,17 @@ extern "C" int64_t kvc_decode_workspace_bytes(int32_t batch, int32_t num_qo_head
   return o_bytes + l_bytes;
 }
 
+extern "C" int64_t kvc_decode_plan_ints(int32_t batch, int32_t num_segments) {
+  if (batch < 0 || num_segments < 0) return -1;
+  return align4(int64_t(num_segments) + 1) + 4 * (int64_t(num_segments) + batch) + batch;
+}
+
 extern "C" int kvc_decode_plan(const int32_t* indptr_host, int32_t batch,
                                int32_t num_qo_heads, int32_t num_kv_heads,
                                int32_t head_dim, int32_t page_size,
-                               int32_t pages_per_partition_hint, int32_t num_cus,
-                               kvc_decode_schedule* sched) {
+                               int32_t num_segments_hint, int32_t num_cus,
+                               kvc_decode_schedule* sched, int32_t* plan_host,
+                               int64_t plan_capacity) {
   KVC_REQUIRE(sched, KVC_ERR_INVALID_ARG, "null schedule");
   KVC_REQUIRE(batch >= 0 && batch <= 65535, KVC_ERR_INVALID_ARG,
               "batch must be in [0, 65535]");
@@ -721,75 +794,116 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, int32_t batch,
   KVC_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
               KVC_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256");
   KVC_REQUIRE(page_size == kPage, KVC_ERR_UNSUPPORTED, "page_size must be 16");
-  KVC_REQUIRE(num_kv_heads <= 65535, KVC_ERR_INVALID_ARG, "too many KV heads");
-
-  int64_t total = 0;
-  int32_t max_pages = 0;
-  int32_t num_empty = 0;
-  for (int b = 0; b < batch; ++b) {
-    const int32_t n = indptr_host[b + 1] - indptr_host[b];
-    KVC_REQUIRE(n >= 0, KVC_ERR_INVALID_ARG, "indptr must be non-decreasing");
-    total += n;
-    max_pages = std::max(max_pages, n);
-    num_empty += n == 0;
-  }
+  KVC_REQUIRE(num_kv_heads <= 65535 * kWaves, KVC_ERR_INVALID_ARG, "too many KV heads");
   KVC_REQUIRE(batch == 0 || indptr_host[0] == 0, KVC_ERR_INVALID_ARG,
               "indptr[0] must be 0");
-
-  int ppp;
-  if (pages_per_partition_hint > 0) {
-    ppp = std::min((pages_per_partition_hint + 3) / 4 * 4, kMaxPagesPerPart);
-  } else {
-    // Aim for ~8 workgroups per CU over (page, KV head) work, in multiples of
-    // 4 pages (one per wave), between 8 and 128 pages per partition.
-    const int64_t cus = num_cus > 0 ? num_cus : 256;
-    const int64_t target = cus * 8;
-    int64_t p = (total * num_kv_heads + target - 1) / std::max<int64_t>(target, 1);
-    p = (p + 3) / 4 * 4;
-    ppp = int(std::min<int64_t>(std::max<int64_t>(p, 8), 128));
+  int32_t num_empty = 0;
+  for (int b = 0; b < batch; ++b) {
+    KVC_REQUIRE(indptr_host[b + 1] >= indptr_host[b], KVC_ERR_INVALID_ARG,
+                "indptr must be non-decreasing");
+    num_empty += indptr_host[b + 1] == indptr_host[b];
   }
+  const int64_t total = batch > 0 ? indptr_host[batch] : 0;
+  const int head_groups = (num_kv_heads + kWaves - 1) / kWaves;
+
+  // Segments per KV-head group: one resident workgroup each, at most
+  // kMaxSegPages pages each, at least one page each.
+  int64_t segs = 0;
+  if (total > 0) {
+    if (num_segments_hint > 0) {
+      segs = num_segments_hint;
+    } else {
+      const int64_t slots = int64_t(num_cus > 0 ? num_cus : 256) *
+                            resident_workgroups_per_cu(group, head_dim);
+      segs = (slots + head_groups - 1) / head_groups;
+    }
+    segs = std::max<int64_t>(segs, (total + kMaxSegPages - 1) / kMaxSegPages);
+    segs = std::min<int64_t>(segs, total);
+  }
+  KVC_REQUIRE(segs <= (int64_t(1) << 30), KVC_ERR_INVALID_ARG, "too many segments");
+  const int64_t need = kvc_decode_plan_ints(batch, int32_t(segs));
   sched->batch = batch;
   sched->num_qo_heads = num_qo_heads;
   sched->num_kv_heads = num_kv_heads;
   sched->head_dim = head_dim;
   sched->page_size = page_size;
-  sched->pages_per_partition = ppp;
-  sched->max_partitions = std::max(1, (max_pages + ppp - 1) / ppp);
+  sched->num_segments = int32_t(segs);
+  sched->num_head_groups = head_groups;
   sched->total_pages = int32_t(total);
   sched->num_empty = num_empty;
+  sched->plan_ints = need;
+  KVC_REQUIRE(plan_host && plan_capacity >= need, KVC_ERR_WORKSPACE,
+              "plan buffer too small: need " + std::to_string(need) + " int32");
+
+  // Plan image: seg_ptr [segs + 1], pieces [num_pieces][4], req_nparts [batch].
+  int32_t* seg_ptr = plan_host;
+  const int64_t pieces_off = align4(segs + 1);
+  int32_t* pieces = plan_host + pieces_off;
+  int32_t* nparts = pieces + 4 * (segs + batch);
+  std::fill(nparts, nparts + batch, 0);
+  int64_t np = 0;
+  int b = 0;
+  seg_ptr[0] = 0;
+  for (int64_t s = 0; s < segs; ++s) {
+    const int64_t g0 = s * total / segs;
+    const int64_t g1 = (s + 1) * total / segs;
+    while (b < batch && indptr_host[b + 1] <= g0) ++b;
+    for (int bb = b; bb < batch && indptr_host[bb] < g1; ++bb) {
+      const int64_t sb = std::max<int64_t>(g0, indptr_host[bb]);
+      const int64_t se = std::min<int64_t>(g1, indptr_host[bb + 1]);
+      if (se > sb) {
+        int32_t* pc = pieces + 4 * np++;
+        pc[0] = bb;
+        pc[1] = int32_t(sb);
+        pc[2] = int32_t(se);
+        pc[3] = nparts[bb]++;
+      }
+    }
+    seg_ptr[s + 1] = int32_t(np);
+  }
+  int32_t max_parts = 1;
+  for (int i = 0; i < batch; ++i) max_parts = std::max(max_parts, nparts[i]);
+  // A request covered by a single piece is written directly (index -1).
+  for (int64_t i = 0; i < np; ++i)
+    if (nparts[pieces[4 * i]] == 1) pieces[4 * i + 3] = -1;
+  sched->num_pieces = int32_t(np);
+  sched->pieces_offset = int32_t(pieces_off);
+  sched->nparts_offset = int32_t(pieces_off + 4 * (segs + batch));
+  sched->max_partitions = max_parts;
   sched->workspace_bytes =
-      kvc_decode_workspace_bytes(batch, num_qo_heads, head_dim, sched->max_partitions);
+      kvc_decode_workspace_bytes(batch, num_qo_heads, head_dim, max_parts);
   return ok();
 }
 
 extern "C" int kvc_batch_decode_run(
-    const kvc_decode_schedule* sched, const void* q, int64_t q_batch_stride,
-    const void* key_cache, const void* value_cache, int64_t cache_block_stride,
-    int64_t cache_token_stride, int64_t num_blocks, const int32_t* indptr,
-    const int32_t* indices, int64_t num_indices, const int32_t* last_page_len,
-    float sm_scale, void* workspace, int64_t workspace_bytes, void* out,
-    int64_t out_batch_stride, float* lse, void* stream) {
+    const kvc_decode_schedule* sched, const int32_t* plan, const void* q,
+    int64_t q_batch_stride, const void* key_cache, const void* value_cache,
+    int64_t cache_block_stride, int64_t cache_token_stride, int64_t num_blocks,
+    const int32_t* indptr, const int32_t* indices, int64_t num_indices,
+    const int32_t* last_page_len, float sm_scale, void* workspace,
+    int64_t workspace_bytes, void* out, int64_t out_batch_stride, float* lse,
+    void* stream) {
   KVC_REQUIRE(sched, KVC_ERR_INVALID_ARG, "null schedule");
   const int batch = sched->batch;
   if (batch == 0) return ok();
-  KVC_REQUIRE(q && key_cache && value_cache && indptr && indices &&
+  KVC_REQUIRE(plan && q && key_cache && value_cache && indptr && indices &&
                   last_page_len && out,
               KVC_ERR_INVALID_ARG, "null pointer");
   const int Hq = sched->num_qo_heads, Hkv = sched->num_kv_heads, D = sched->head_dim;
   KVC_REQUIRE(Hkv > 0 && Hq % Hkv == 0, KVC_ERR_INVALID_ARG, "bad head counts");
   const int group = Hq / Hkv;
   KVC_REQUIRE(sched->page_size == kPage, KVC_ERR_UNSUPPORTED, "page_size must be 16");
-  KVC_REQUIRE(sched->pages_per_partition > 0 && sched->pages_per_partition % 4 == 0 &&
-                  sched->pages_per_partition <= kMaxPagesPerPart &&
-                  sched->max_partitions >= 1 && sched->max_partitions <= 65535,
+  KVC_REQUIRE(sched->num_segments >= 0 && sched->max_partitions >= 1 &&
+                  sched->num_head_groups == (Hkv + kWaves - 1) / kWaves &&
+                  sched->plan_ints == kvc_decode_plan_ints(batch, sched->num_segments),
               KVC_ERR_INVALID_ARG, "schedule not produced by kvc_decode_plan");
-  KVC_REQUIRE(num_blocks > 0 && num_indices >= 0, KVC_ERR_INVALID_ARG,
-              "bad num_blocks / num_indices");
+  KVC_REQUIRE(num_blocks > 0 && num_indices >= sched->total_pages, KVC_ERR_INVALID_ARG,
+              "bad num_blocks or fewer indices than planned pages");
   KVC_REQUIRE(cache_token_stride >= int64_t(Hkv) * D &&
                   cache_block_stride >= cache_token_stride * kPage,
               KVC_ERR_INVALID_ARG, "cache strides smaller than the block");
-  KVC_REQUIRE(cache_token_stride * kPage < (int64_t(1) << 31), KVC_ERR_INVALID_ARG,
-              "a cache block spans more than 2^31 elements");
+  KVC_REQUIRE(cache_token_stride * kPage * 2 < (int64_t(1) << 31), KVC_ERR_INVALID_ARG,
+              "a cache block spans more than 2 GiB");
   KVC_REQUIRE(q_batch_stride >= int64_t(Hq) * D && out_batch_stride >= int64_t(Hq) * D,
               KVC_ERR_INVALID_ARG, "q/out batch stride smaller than Hq*head_dim");
   KVC_REQUIRE(sm_scale > 0.f, KVC_ERR_INVALID_ARG, "sm_scale must be positive");
@@ -800,6 +914,9 @@ extern "C" int kvc_batch_decode_run(
                   (cache_block_stride * 2) % vec_bytes == 0 &&
                   (cache_token_stride * 2) % vec_bytes == 0,
               KVC_ERR_ALIGNMENT, "q/cache pointers or strides not vector aligned");
+  KVC_REQUIRE(aligned(out, 4) && out_batch_stride % 2 == 0 && aligned(plan, 16),
+              KVC_ERR_ALIGNMENT, "out must be 4-byte aligned with an even batch stride, "
+                                 "plan 16-byte aligned");
   const int64_t need = kvc_decode_workspace_bytes(batch, Hq, D, sched->max_partitions);
   KVC_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), KVC_ERR_WORKSPACE,
               "decode workspace too small: need " + std::to_string(need) + " bytes");
@@ -816,9 +933,10 @@ extern "C" int kvc_batch_decode_run(
   a.indices = indices;
   a.num_indices = num_indices;
   a.last_page_len = last_page_len;
+  a.seg_ptr = plan;
+  a.pieces = reinterpret_cast<const int4*>(plan + sched->pieces_offset);
   a.scale_log2 = sm_scale * kLog2e;
   a.num_kv_heads = Hkv;
-  a.pages_per_part = sched->pages_per_partition;
   a.max_parts = sched->max_partitions;
   const int64_t rows = int64_t(batch) * Hq * sched->max_partitions;
   a.part_o = need ? static_cast<float*>(workspace) : nullptr;
@@ -830,23 +948,25 @@ extern "C" int kvc_batch_decode_run(
   a.lse = lse;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
-  bool launched = false;
-  if (D == 128) launched = dispatch_group<128>(group, a, batch, s);
-  else if (D == 64) launched = dispatch_group<64>(group, a, batch, s);
-  else if (D == 256) launched = dispatch_group<256>(group, a, batch, s);
-  KVC_REQUIRE(launched, KVC_ERR_UNSUPPORTED,
-              "unsupported (group, head_dim) = (" + std::to_string(group) + ", " +
-                  std::to_string(D) + ")");
-  KVC_LAUNCH_CHECK();
-  // Single-partition requests were written by the partition kernel; the merge
+  if (sched->num_segments > 0) {
+    bool launched = false;
+    const int segs = sched->num_segments, hg = sched->num_head_groups;
+    if (D == 128) launched = dispatch_group<128>(group, a, segs, hg, s);
+    else if (D == 64) launched = dispatch_group<64>(group, a, segs, hg, s);
+    else if (D == 256) launched = dispatch_group<256>(group, a, segs, hg, s);
+    KVC_REQUIRE(launched, KVC_ERR_UNSUPPORTED,
+                "unsupported (group, head_dim) = (" + std::to_string(group) + ", " +
+                    std::to_string(D) + ")");
+    KVC_LAUNCH_CHECK();
+  }
+  // Single-piece requests were written by the streaming kernel; the merge
   // pass is needed for split requests and to zero empty ones.
   if (sched->max_partitions == 1 && sched->num_empty == 0) return ok();
 
   MergeArgs m;
   m.part_o = a.part_o;
   m.part_lse = a.part_lse;
-  m.indptr = indptr;
-  m.pages_per_part = a.pages_per_part;
+  m.req_nparts = plan + sched->nparts_offset;
   m.max_parts = a.max_parts;
   m.num_kv_heads = Hkv;
   m.group = group;

@@ -6,10 +6,11 @@
 :2069-2070 and :3907-3909 run) and launches the HIP kernels of
 csrc/decode.hip through libkvc.so.
 
-``plan`` is host work (plus small H2D copies), like FlashInfer's: it reads the
-host indptr, picks the split-K partition size and stages indptr / indices /
-last_page_len on the device.  ``run`` launches the partition kernel and, when a
-request spans more than one partition, the merge kernel.  ``plan`` must be
+``plan`` is host work (plus one small H2D copy), like FlashInfer's: it reads
+the host indptr, cuts the batch's pages into equal segments (the balanced
+split-KV schedule of kvc_decode_plan) and stages the schedule, indptr, indices
+and last_page_len on the device.  ``run`` launches the streaming kernel and,
+when a request spans more than one segment, the merge kernel.  ``plan`` must be
 called again whenever the sequence lengths change (the engine re-plans every
 step after bumping ``_seq_lens_cpu``, moe_engine.py:3554-3556).
 """
@@ -44,7 +45,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
                  paged_kv_indptr_buffer: Optional[torch.Tensor] = None,
                  paged_kv_indices_buffer: Optional[torch.Tensor] = None,
                  paged_kv_last_page_len_buffer: Optional[torch.Tensor] = None,
-                 pages_per_partition: Optional[int] = None):
+                 num_segments: Optional[int] = None):
         if kv_layout != "NHD":
             _fail(f"kv_layout={kv_layout!r} is not supported (only 'NHD')")
         if not float_workspace_buffer.is_cuda:
@@ -55,7 +56,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
         self._indptr_buf = paged_kv_indptr_buffer
         self._indices_buf = paged_kv_indices_buffer
         self._lpl_buf = paged_kv_last_page_len_buffer
-        self._ppp_hint = int(pages_per_partition or 0)
+        self._segments_hint = int(num_segments or 0)
         self._num_cus = torch.cuda.get_device_properties(self._device).multi_processor_count
         self._sched: Optional[_lib.KvcDecodeSchedule] = None
         self._indices = None
@@ -102,35 +103,48 @@ class BatchDecodeWithPagedKVCacheWrapper:
 
         indptr_host = indptr[: batch + 1].to("cpu").contiguous() if indptr.is_cuda \
             else indptr[: batch + 1].contiguous()
-        sched = _lib.KvcDecodeSchedule()
-        _lib.call("kvc_decode_plan", indptr_host.data_ptr(), batch, num_qo_heads, num_kv_heads,
-                  head_dim, page_size, self._ppp_hint, self._num_cus, sched)
-        ws = self._workspace.numel() * self._workspace.element_size()
-        if sched.workspace_bytes > ws:
-            _fail(f"decode workspace too small: need {sched.workspace_bytes} bytes, have {ws}")
         total = int(indptr_host[-1]) if batch > 0 else 0
         if indices.numel() < total:
             _fail(f"indices has {indices.numel()} entries, indptr[-1] = {total}")
 
+        # Host-side schedule (kvc_decode_plan), written straight into the
+        # pinned staging tensor of the one H2D copy of the batch metadata:
+        #   [plan image | indptr | last_page_len].  A fresh pinned tensor from
+        # torch's caching host allocator stays alive until its async copy has
+        # run, so plan() never waits for the GPU.
+        lib = _lib.load()
+        sched = _lib.KvcDecodeSchedule()
+        cap = lib.kvc_decode_plan_ints(batch, max(self._segments_hint, 4 * self._num_cus))
+        for _ in range(2):
+            cap4 = (cap + 3) // 4 * 4
+            hs = torch.empty(cap4 + 2 * batch + 1, dtype=torch.int32, pin_memory=True)
+            st = lib.kvc_decode_plan(indptr_host.data_ptr(), batch, num_qo_heads, num_kv_heads,
+                                     head_dim, page_size, self._segments_hint, self._num_cus,
+                                     sched, hs.data_ptr(), cap4)
+            if st == _lib.KVC_ERR_WORKSPACE and sched.plan_ints > cap4:
+                cap = sched.plan_ints
+                continue
+            _lib.check("kvc_decode_plan", st)
+            break
+        ws = self._workspace.numel() * self._workspace.element_size()
+        if sched.workspace_bytes > ws:
+            _fail(f"decode workspace too small: need {sched.workspace_bytes} bytes, have {ws}")
+
         dev = self._device
-        # Device copies of indptr / last_page_len, staged through a fresh
-        # pinned tensor: torch's caching host allocator keeps it alive until
-        # the async copy has run, so plan() never waits for the GPU.
-        n_meta = 2 * batch + 1
-        hs = torch.empty(n_meta, dtype=torch.int32, pin_memory=True)
-        hs[: batch + 1].copy_(indptr_host)
-        hs[batch + 1:].copy_(last_page_len[:batch])
+        hs[cap4: cap4 + batch + 1].copy_(indptr_host)
+        hs[cap4 + batch + 1:].copy_(last_page_len[:batch])
         dm = hs.to(dev, non_blocking=True)
+        plan_dev = dm[:cap4]
         if self._indptr_buf is not None:
-            self._indptr_buf[: batch + 1].copy_(dm[: batch + 1])
+            self._indptr_buf[: batch + 1].copy_(dm[cap4: cap4 + batch + 1])
             indptr_dev = self._indptr_buf
         else:
-            indptr_dev = dm[: batch + 1]
+            indptr_dev = dm[cap4: cap4 + batch + 1]
         if self._lpl_buf is not None:
-            self._lpl_buf[:batch].copy_(dm[batch + 1: n_meta])
+            self._lpl_buf[:batch].copy_(dm[cap4 + batch + 1:])
             lpl_dev = self._lpl_buf
         else:
-            lpl_dev = dm[batch + 1: n_meta]
+            lpl_dev = dm[cap4 + batch + 1:]
         if indices.is_cuda:
             if indices.device != dev:
                 _fail("indices on a different device than the workspace")
@@ -148,6 +162,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
             indices_dev = indices_dev.contiguous()
 
         self._sched = sched
+        self._plan_dev = plan_dev
         self._indptr = indptr_dev
         self._lpl = lpl_dev
         self._indices = indices_dev
@@ -216,7 +231,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
             _fail("lse must be contiguous float32 [B, num_qo_heads]")
         s = stream if stream is not None else torch.cuda.current_stream(self._device)
         ws = self._workspace
-        _lib.call("kvc_batch_decode_run", self._sched, q.data_ptr(), q.stride(0),
+        _lib.call("kvc_batch_decode_run", self._sched, self._plan_dev.data_ptr(),
+                  q.data_ptr(), q.stride(0),
                   k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
                   k_cache.shape[0], self._indptr.data_ptr(), self._indices.data_ptr(),
                   self._num_indices, self._lpl.data_ptr(), self._sm_scale, ws.data_ptr(),

@@ -83,7 +83,7 @@ class PagedKVCache:
                  free_page_order: Optional[Iterable[int]] = None,
                  workspace_bytes: int = 128 * 1024 * 1024,
                  staging_bytes: int = 256 * 1024 * 1024,
-                 pages_per_partition: Optional[int] = None):
+                 num_segments: Optional[int] = None):
         if page_size != 16:
             raise ValueError("page_size must be 16 (the engine's page size)")
         self.device = torch.device(device)
@@ -115,7 +115,7 @@ class PagedKVCache:
                               free_order=free_page_order) if self._dynamic_pages else None
 
         self._workspace_bytes = workspace_bytes
-        self._ppp = pages_per_partition
+        self._segments = num_segments
         self._decode_wrapper: Optional[BatchDecodeWithPagedKVCacheWrapper] = None
         if self.device.type == "cuda":
             self._init_step_buffers()
@@ -137,7 +137,7 @@ class PagedKVCache:
                                           device=self.device)
         self._decode_wrapper = BatchDecodeWithPagedKVCacheWrapper(
             self._workspace_buf, kv_layout="NHD", use_cuda_graph=False,
-            pages_per_partition=self._ppp)
+            num_segments=self._segments)
         self._plan_indices_gpu = torch.zeros(self.max_seqs * self.max_pages_per_seq,
                                              dtype=torch.int32, device=self.device)
 

@@ -102,14 +102,21 @@ int kvc_gather_kv(
  *   out[b][hq] = softmax_t(sm_scale * q[b][hq] . K[t][hq/group]) . V[t][hq/group]
  * group = num_qo_heads / num_kv_heads.  Optional lse[b][hq] receives the
  * natural-log log-sum-exp of the scaled logits (-inf for an empty request).
- * The context is split into partitions of pages_per_partition pages; partial
- * results go to the workspace and are merged with the log-sum-exp rule of
- * src/dense/offload_kv_attn.py:24-39.
  *
- * kvc_decode_plan is host-only (no device access): it picks the partition size
- * from the host copy of indptr, like FlashInfer plan() which also reads a host
- * indptr.  pages_per_partition_hint > 0 forces the size (rounded up to a
- * multiple of 4).  kvc_decode_workspace_bytes sizes the workspace.
+ * kvc_decode_plan is host-only (no device access), like FlashInfer plan(),
+ * which also reads a host indptr.  It cuts the batch's flattened page list
+ * into num_segments equal segments per group of 4 KV heads (by default one
+ * per workgroup the GPU holds at once; num_segments_hint > 0 forces the
+ * count) and writes the plan image into plan_host:
+ *   [0, num_segments]            segment -> first piece
+ *   [pieces_offset, +4*pieces)   (request, first slot, end slot, partial or -1)
+ *   [nparts_offset, +batch)      pieces per request
+ * (plan_ints int32 in total; kvc_decode_plan_ints gives the size for a
+ * segment count).  If plan_capacity is too small it fills schedule->plan_ints
+ * and returns KVC_ERR_WORKSPACE.  The caller copies the image to the device
+ * and passes it to kvc_batch_decode_run.  Pieces of one request are merged
+ * with the log-sum-exp rule of src/dense/offload_kv_attn.py:24-39;
+ * kvc_decode_workspace_bytes sizes the fp32 partials.
  * ---------------------------------------------------------------------- */
 typedef struct kvc_decode_schedule {
   int32_t batch;
@@ -117,24 +124,34 @@ typedef struct kvc_decode_schedule {
   int32_t num_kv_heads;
   int32_t head_dim;
   int32_t page_size;
-  int32_t pages_per_partition;
-  int32_t max_partitions;     /* max over requests of ceil(pages/ppp) */
-  int32_t total_pages;        /* indptr[batch]                         */
-  int32_t num_empty;          /* requests with no pages (output zero)  */
-  int64_t workspace_bytes;    /* bytes kvc_batch_decode_run will use   */
+  int32_t num_segments;     /* segments per group of 4 KV heads            */
+  int32_t num_head_groups;  /* ceil(num_kv_heads / 4)                      */
+  int32_t num_pieces;
+  int32_t pieces_offset;    /* int32 offsets inside the plan image         */
+  int32_t nparts_offset;
+  int32_t max_partitions;   /* max pieces of one request                   */
+  int32_t total_pages;      /* indptr[batch]                               */
+  int32_t num_empty;        /* requests with no pages (output zero)        */
+  int32_t reserved;
+  int64_t plan_ints;        /* int32 entries of the plan image             */
+  int64_t workspace_bytes;  /* bytes kvc_batch_decode_run will use         */
 } kvc_decode_schedule;
+
+int64_t kvc_decode_plan_ints(int32_t batch, int32_t num_segments);
 
 int kvc_decode_plan(const int32_t* indptr_host, int32_t batch,
                     int32_t num_qo_heads, int32_t num_kv_heads,
                     int32_t head_dim, int32_t page_size,
-                    int32_t pages_per_partition_hint, int32_t num_cus,
-                    kvc_decode_schedule* schedule);
+                    int32_t num_segments_hint, int32_t num_cus,
+                    kvc_decode_schedule* schedule, int32_t* plan_host,
+                    int64_t plan_capacity);
 
 int64_t kvc_decode_workspace_bytes(int32_t batch, int32_t num_qo_heads,
                                    int32_t head_dim, int32_t max_partitions);
 
+/* plan: the device copy (16-byte aligned) of the image kvc_decode_plan wrote. */
 int kvc_batch_decode_run(
-    const kvc_decode_schedule* schedule,
+    const kvc_decode_schedule* schedule, const int32_t* plan,
     const void* q, int64_t q_batch_stride,
     const void* key_cache, const void* value_cache,
     int64_t cache_block_stride, int64_t cache_token_stride,

@@ -58,37 +58,111 @@ def test_version_and_status_strings(lib):
     assert b"workspace" in lib.kvc_status_string(4)
 
 
-def test_decode_plan_is_host_only_and_splits_partitions(lib):
-    lens = np.array([1, 16, 17, 4096, 0], np.int64)
-    pages = (lens + 15) // 16
+def _plan(lib, lens, hq=32, hkv=8, d=128, hint=0, cus=256):
+    pages = (np.asarray(lens, np.int64) + 15) // 16
     indptr = np.zeros(len(lens) + 1, np.int32)
     np.cumsum(pages, out=indptr[1:])
     sched = _lib.KvcDecodeSchedule()
-    st = lib.kvc_decode_plan(indptr.ctypes.data, len(lens), 32, 8, 128, 16, 8, 256,
-                             ctypes.byref(sched))
-    assert st == 0
-    assert sched.pages_per_partition == 8
-    assert sched.max_partitions == 32          # 256 pages / 8
-    assert sched.total_pages == int(pages.sum())
+    cap = lib.kvc_decode_plan_ints(len(lens), max(hint, 4 * cus))
+    img = np.zeros(cap, np.int32)
+    st = lib.kvc_decode_plan(indptr.ctypes.data, len(lens), hq, hkv, d, 16, hint, cus,
+                             ctypes.byref(sched), img.ctypes.data, cap)
+    assert st == 0, lib.kvc_last_error()
+    return indptr, sched, img
+
+
+def _check_plan_image(indptr, sched, img):
+    """Segments are contiguous, equal to within one page, at most 256 pages,
+    and their pieces tile every request's pages exactly once, numbered
+    0..n-1 per request (-1 when a request is a single piece)."""
+    S = sched.num_segments
+    seg_ptr = img[:S + 1]
+    pieces = img[sched.pieces_offset:sched.pieces_offset + 4 * sched.num_pieces].reshape(-1, 4)
+    nparts = img[sched.nparts_offset:sched.nparts_offset + sched.batch]
+    total = int(indptr[-1])
+    assert sched.total_pages == total and seg_ptr[0] == 0 and seg_ptr[-1] == sched.num_pieces
+    lengths = []
+    for s in range(S):
+        ps = pieces[seg_ptr[s]:seg_ptr[s + 1]]
+        assert len(ps) >= 1
+        assert (ps[1:, 1] == ps[:-1, 2]).all()                 # contiguous slots
+        assert ps[0, 1] == s * total // S and ps[-1, 2] == (s + 1) * total // S
+        lengths.append(ps[-1, 2] - ps[0, 1])
+    assert max(lengths) - min(lengths) <= 1 and max(lengths) <= 256
+    for b in range(sched.batch):
+        mine = pieces[pieces[:, 0] == b]
+        assert len(mine) == nparts[b]
+        if len(mine) == 0:
+            assert indptr[b + 1] == indptr[b]
+            continue
+        assert mine[0, 1] == indptr[b] and mine[-1, 2] == indptr[b + 1]
+        assert (mine[1:, 1] == mine[:-1, 2]).all()
+        if len(mine) == 1:
+            assert mine[0, 3] == -1
+        else:
+            assert mine[:, 3].tolist() == list(range(len(mine)))
+    assert sched.max_partitions == max(1, int(nparts.max()))
+
+
+def test_decode_plan_is_host_only_and_balanced(lib):
+    lens = [1, 16, 17, 4096, 0, 300, 2049, 33]
+    indptr, sched, img = _plan(lib, lens, hint=40)
+    assert sched.num_segments == 40 and sched.num_head_groups == 2
     assert sched.num_empty == 1
-    assert sched.workspace_bytes == lib.kvc_decode_workspace_bytes(len(lens), 32, 128, 32)
-    # rounding of the hint to a multiple of 4 and the upper clamp
-    lib.kvc_decode_plan(indptr.ctypes.data, len(lens), 32, 8, 128, 16, 5, 256, ctypes.byref(sched))
-    assert sched.pages_per_partition == 8
-    lib.kvc_decode_plan(indptr.ctypes.data, len(lens), 32, 8, 128, 16, 100000, 256,
-                        ctypes.byref(sched))
-    assert sched.pages_per_partition == 256 and sched.max_partitions == 1
+    _check_plan_image(indptr, sched, img)
+    assert sched.workspace_bytes == lib.kvc_decode_workspace_bytes(
+        len(lens), 32, 128, sched.max_partitions)
+    # default: one segment per resident workgroup (256 CUs x 2) per 2 head groups
+    indptr, sched, img = _plan(lib, [3000] * 64)
+    assert sched.num_segments == 256
+    _check_plan_image(indptr, sched, img)
+    # segments never exceed 256 pages, never hold less than one page
+    indptr, sched, img = _plan(lib, [16 * 5000], hint=2)
+    assert sched.num_segments == 20
+    _check_plan_image(indptr, sched, img)
+    indptr, sched, img = _plan(lib, [40, 1], hint=1000)
+    assert sched.num_segments == 4
+    _check_plan_image(indptr, sched, img)
+
+
+def test_decode_plan_random_batches(lib):
+    rng = np.random.default_rng(0)
+    for trial in range(30):
+        lens = rng.integers(0, 3000, rng.integers(1, 80)).tolist()
+        hkv = int(rng.choice([1, 4, 8, 16]))
+        hint = int(rng.choice([0, 1, 7, 64, 333]))
+        indptr, sched, img = _plan(lib, lens, hq=hkv * 4, hkv=hkv, hint=hint,
+                                   cus=int(rng.integers(1, 300)))
+        if indptr[-1] == 0:
+            assert sched.num_segments == 0
+            continue
+        _check_plan_image(indptr, sched, img)
+
+
+def test_decode_plan_reports_the_needed_capacity(lib):
+    indptr = np.array([0, 100, 100, 300], np.int32)
+    sched = _lib.KvcDecodeSchedule()
+    small = np.zeros(4, np.int32)
+    st = lib.kvc_decode_plan(indptr.ctypes.data, 3, 32, 8, 128, 16, 50, 256, ctypes.byref(sched),
+                             small.ctypes.data, 4)
+    assert st == 4 and sched.plan_ints == lib.kvc_decode_plan_ints(3, 50)
+    assert b"plan buffer too small" in lib.kvc_last_error()
 
 
 def test_decode_plan_rejects_bad_shapes(lib):
     indptr = np.array([0, 3], np.int32)
     sched = _lib.KvcDecodeSchedule()
-    assert lib.kvc_decode_plan(indptr.ctypes.data, 1, 12, 8, 128, 16, 0, 256, ctypes.byref(sched)) == 1
+    img = np.zeros(4096, np.int32)
+
+    def plan(hq, hkv, d, ps, ip=indptr, batch=1):
+        return lib.kvc_decode_plan(ip.ctypes.data, batch, hq, hkv, d, ps, 0, 256,
+                                   ctypes.byref(sched), img.ctypes.data, img.size)
+
+    assert plan(12, 8, 128, 16) == 1
     assert b"multiple" in lib.kvc_last_error()
-    assert lib.kvc_decode_plan(indptr.ctypes.data, 1, 32, 8, 96, 16, 0, 256, ctypes.byref(sched)) == 2
-    assert lib.kvc_decode_plan(indptr.ctypes.data, 1, 32, 8, 128, 32, 0, 256, ctypes.byref(sched)) == 2
-    bad = np.array([0, 5, 3], np.int32)
-    assert lib.kvc_decode_plan(bad.ctypes.data, 2, 32, 8, 128, 16, 0, 256, ctypes.byref(sched)) == 1
+    assert plan(32, 8, 96, 16) == 2
+    assert plan(32, 8, 128, 32) == 2
+    assert plan(32, 8, 128, 16, np.array([0, 5, 3], np.int32), 2) == 1
     assert b"non-decreasing" in lib.kvc_last_error()
 
 

@@ -33,9 +33,9 @@ def _paged(lens, hkv, d, seed, total_pages=None, device=None, fill_std=1.0):
     return kc, vc, pool.block_table, indptr, indices, lpl
 
 
-def _run(gpu, q, kc, vc, indptr, indices, lpl, hq, hkv, d, ppp=None, return_lse=True):
+def _run(gpu, q, kc, vc, indptr, indices, lpl, hq, hkv, d, segs=None, return_lse=True):
     w = BatchDecodeWithPagedKVCacheWrapper(torch.empty(WS, dtype=torch.uint8, device=gpu),
-                                           pages_per_partition=ppp)
+                                           num_segments=segs)
     w.plan(torch.from_numpy(indptr), torch.from_numpy(indices).to(gpu), torch.from_numpy(lpl),
            num_qo_heads=hq, num_kv_heads=hkv, head_dim=d, page_size=16)
     res = w.run(q, (kc, vc), return_lse=return_lse)
@@ -102,14 +102,18 @@ def test_decode_ignores_nan_in_slots_past_the_end(gpu):
     assert_attn_close(out.float().cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("ppp", [4, 8, 12, 64, None])
-def test_decode_partition_sizes_agree(gpu, ppp):
+@pytest.mark.parametrize("segs", [1, 3, 8, 41, 1000, None])
+def test_decode_segment_counts_agree(gpu, segs):
+    """Any split of the batch into segments (one request spread over many
+    pieces, many requests in one segment) gives the same attention."""
     lens = [1, 15, 16, 17, 64, 100, 511, 512, 513, 2000]
     kc, vc, bt, indptr, indices, lpl = _paged(lens, 8, 128, 6)
     q = randn_bf16((len(lens), 32, 128), 7, device=gpu)
-    (out, lse), w = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, 32, 8, 128, ppp=ppp)
-    if ppp is not None:
-        assert w.schedule.pages_per_partition == (ppp + 3) // 4 * 4
+    (out, lse), w = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, 32, 8, 128,
+                         segs=segs)
+    if segs is not None:
+        total = int(indptr[-1])
+        assert w.schedule.num_segments == min(max(segs, (total + 255) // 256), total)
     ref, ref_lse = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
     assert_attn_close(out.float().cpu().numpy(), ref)
     assert np.allclose(lse.cpu().numpy(), ref_lse, atol=1e-3, rtol=1e-4)
@@ -122,7 +126,7 @@ def test_decode_group_sizes_and_head_dims(gpu, group, d):
     lens = [3, 77, 300, 1025]
     kc, vc, bt, indptr, indices, lpl = _paged(lens, hkv, d, 8)
     q = randn_bf16((len(lens), hq, d), 9, device=gpu)
-    (out, _), _ = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, hq, hkv, d, ppp=8)
+    (out, _), _ = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, hq, hkv, d, segs=9)
     ref, _ = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
     assert_attn_close(out.float().cpu().numpy(), ref)
 
@@ -133,8 +137,9 @@ def test_decode_empty_request_gives_zero_and_neg_inf_lse(gpu):
     indptr = np.array([0, 0, 3, 3], np.int32)
     lpl = np.array([0, 8, 0], np.int32)
     q = randn_bf16((3, 32, 128), 11, device=gpu)
-    for ppp in (None, 4):
-        (out, lse), _ = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, 32, 8, 128, ppp=ppp)
+    for segs in (None, 2):
+        (out, lse), _ = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, 32, 8, 128,
+                             segs=segs)
         assert int(out[0].abs().sum()) == 0 and int(out[2].abs().sum()) == 0
         assert torch.isneginf(lse[0]).all() and torch.isneginf(lse[2]).all()
         ref, _ = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
