@@ -42,6 +42,22 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
+# rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the configuration-2 decode launch
+# (calibrated HBM bytes per launch), written from `--mode decode2` runs.
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_lds_kernel_cfg2_mixtral_decode.md")
+
+
+def profiled_traffic():
+    """HBM bytes per decode launch measured by the committed counter profile,
+    or None when the summary is absent."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg: str) -> None:
@@ -163,7 +179,7 @@ def run_step_bench(torch, args):
         "ms_per_step": ms_per_step,
         "value": step_gbps,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": profiled_traffic(),
                      "kernel": "decode_lds_kernel<4> + decode_merge_kernel<128>",
                      "avg_launch_us": avg_ms * 1e3, "algorithmic_bytes_per_launch": avg_bytes,
                      "segments": sched.num_segments, "head_groups": sched.num_head_groups,

@@ -47,34 +47,40 @@ __global__ __launch_bounds__(kThreads) void append_vec16_kernel(AppendArgs a) {
   const uint32_t total = uint32_t(a.num_tokens) * per_tok;
   const uint32_t base = blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
 
+  // The source rows do not depend on the slot: issue their loads together
+  // with the slot loads, so a small append costs one memory round trip
+  // before the stores instead of two.
   uint4 buf[kUnroll];
-  char* dst[kUnroll];
+  int64_t slot[kUnroll];
+  uint32_t tok[kUnroll], chunk[kUnroll];
+  bool is_v[kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const uint32_t item = base + uint32_t(u) * kThreads;
-    dst[u] = nullptr;
+    slot[u] = -1;
     if (item >= total) continue;
-    const uint32_t tok = item / per_tok;
-    const uint32_t rem = item - tok * per_tok;
-    const bool is_v = rem >= rc;
-    const uint32_t chunk = is_v ? rem - rc : rem;
-    const int64_t slot = a.slots[tok];
-    if (slot < 0) continue;  // padding token
-    if (slot >= a.num_slots) {
-      if (a.oob_count && chunk == 0 && !is_v) atomicAdd(a.oob_count, 1);
-      continue;
-    }
-    const int64_t blk = slot / a.block_size;
-    const int64_t off = slot - blk * a.block_size;
-    const char* src = (is_v ? a.value + int64_t(tok) * a.value_stride
-                            : a.key + int64_t(tok) * a.key_stride) + chunk * 16u;
+    tok[u] = item / per_tok;
+    const uint32_t rem = item - tok[u] * per_tok;
+    is_v[u] = rem >= rc;
+    chunk[u] = is_v[u] ? rem - rc : rem;
+    slot[u] = a.slots[tok[u]];
+    const char* src = (is_v[u] ? a.value + int64_t(tok[u]) * a.value_stride
+                               : a.key + int64_t(tok[u]) * a.key_stride) + chunk[u] * 16u;
     buf[u] = *reinterpret_cast<const uint4*>(src);
-    dst[u] = (is_v ? a.value_cache : a.key_cache) + blk * a.block_stride +
-             off * a.token_stride + chunk * 16u;
   }
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u)
-    if (dst[u]) *reinterpret_cast<uint4*>(dst[u]) = buf[u];
+  for (int u = 0; u < kUnroll; ++u) {
+    if (slot[u] < 0) continue;  // padding token (or past the end)
+    if (slot[u] >= a.num_slots) {
+      if (a.oob_count && chunk[u] == 0 && !is_v[u]) atomicAdd(a.oob_count, 1);
+      continue;
+    }
+    const int64_t blk = slot[u] / a.block_size;
+    const int64_t off = slot[u] - blk * a.block_size;
+    char* dst = (is_v[u] ? a.value_cache : a.key_cache) + blk * a.block_stride +
+                off * a.token_stride + chunk[u] * 16u;
+    *reinterpret_cast<uint4*>(dst) = buf[u];
+  }
 }
 
 // Fallback for rows that are not a whole number of aligned 16-byte chunks:
