@@ -48,7 +48,7 @@ class KvcDecodeSchedule(ctypes.Structure):
         ("max_partitions", c_int32),
         ("total_pages", c_int32),
         ("num_empty", c_int32),
-        ("reserved", c_int32),
+        ("heads_per_group", c_int32),
         ("plan_ints", c_int64),
         ("workspace_bytes", c_int64),
     ]

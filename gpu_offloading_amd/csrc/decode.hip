@@ -21,28 +21,31 @@
 // otherwise each piece leaves an fp32 partial + log2-sum-exp in the workspace
 // and decode_merge_kernel folds them.
 //
-// Grid (S, ceil(Hkv / 4)), 256 threads: wave w of workgroup (s, y) owns KV
-// head 4y + w of segment s and serves all `group` query heads of that KV head,
-// so K/V are read from HBM exactly once.  The four waves of a workgroup read
-// four neighbouring heads of the same pages (1 KB contiguous per token row).
-// Waves are independent: no workgroup barrier.  A wave's page ids are loaded
-// once, one per lane (4 registers: up to 256 pages), and broadcast with
-// v_readlane, so no dependent global load sits in the streaming loop.
-//
-// head_dim 128 (the reference models) uses decode_lds_kernel: each wave stages
-// one page (16 tokens x 256 B of K and of V) from HBM through registers into
-// its own LDS tile; the next two pages are in flight in two register stages
-// while a page is consumed.  Tile rows are padded to 272 B, which keeps both
-// read patterns below free of LDS bank conflicts:
+// head_dim 128 (the reference models) uses decode_lds_kernel<G, HPW>: grid
+// (S, Hkv / HPW), one wave per KV head, HPW = 8 heads per workgroup when the
+// heads divide evenly (else 1).  Every wave serves all `group` query heads of
+// its KV head, so K/V are read from HBM exactly once.  The waves stage each
+// page together: wave w loads 256 consecutive 16-byte chunks of the page's
+// (token row x head slice) image (two whole 2 KB token rows for Mixtral), so
+// the workgroup reads the page's K and V blocks as contiguous runs, into a
+// double-buffered LDS tile; one barrier per page; the next two pages are in
+// flight in two register stages meanwhile.  Tile rows are padded by 16 B,
+// which keeps both read patterns below free of LDS bank conflicts and makes
+// every LDS address a lane base plus an immediate:
 //   q.k : lane (token t, query head g) computes the whole 128-dim dot product
 //         with v_dot2_f32_bf16 from 16 ds_read_b128 of row t (the four lanes
 //         of a token read the same address); no cross-lane reduction;
 //   p.v : lane l owns dims 2l, 2l+1 for every query head; per token one
 //         ds_read_b32 of V and one broadcast read of p[t][0..G).
 // Softmax statistics live per 16-lane DPP row (one query head per row).
-// head_dim 64 and 256 use decode_reg_kernel, which keeps K/V in registers:
-// lane (row r, column c) holds 16 B of tokens r, r+4, r+8, r+12 and q.k is
-// reduced over the 16 lanes of a DPP row.
+// A wave's page ids are loaded once, one per lane (4 registers: up to 256
+// pages), and broadcast with v_readlane, so no dependent global load sits in
+// the streaming loop.
+//
+// head_dim 64 and 256 use decode_reg_kernel: grid (S, ceil(Hkv / 4)), one
+// wave per KV head, no barrier; K/V stay in registers: lane (row r, column c)
+// holds 16 B of tokens r, r+4, r+8, r+12 and q.k is reduced over the 16 lanes
+// of a DPP row.
 #include "kvc_common.h"
 
 #include <algorithm>
@@ -51,8 +54,8 @@
 namespace kvc {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;  // KV heads per workgroup
+constexpr int kThreads = 256;          // register kernel workgroup
+constexpr int kWaves = kThreads / 64;  // KV heads per register-kernel workgroup
 constexpr int kPage = 16;              // tokens per page (the engine's page_size)
 constexpr int kTokPerRow = 4;          // register kernel: tokens of a page per 16-lane row
 constexpr int kIdRegs = 4;             // page-id registers per lane
@@ -189,47 +192,63 @@ struct LdsCfg {
   static constexpr int CH = 16 / NS;            // 16-byte chunks of a K row per lane
 };
 
-// One wave's LDS tile: K and V of one page of one KV head, 16 token rows of
-// 256 B each stored with a 16 B pad (272 B row pitch), so that the 16 rows
-// read by one instruction start on 16 different 4-bank groups, and every
-// lane address is a per-lane base plus an immediate offset.
-constexpr int kRowPitch = 17;  // uint4 per padded row
-struct __align__(16) PageTile {
-  uint4 k[kPage * kRowPitch];
-  uint4 v[kPage * kRowPitch];
-  float p[kPage * 8];  // softmax weights p[token][query head], G <= 8
+// The LDS tile of one page for the HPW KV heads of a workgroup: K and V, 16
+// token rows of HPW x 256 B, each row padded by 16 B.  With the pad, the 16
+// rows read by one q.k instruction start on 16 different 4-bank groups, and
+// every lane address is a lane base plus an immediate offset.
+template <int HPW>
+struct BlockTile {
+  static constexpr int kRowBytes = HPW * 256 + 16;
+  static constexpr int kRowChunks = kRowBytes / 16;
+  uint4 k[kPage * kRowChunks];
+  uint4 v[kPage * kRowChunks];
 };
 
-template <int G>
-__global__ __launch_bounds__(kThreads) void decode_lds_kernel(DecodeArgs a) {
+// Workgroup = HPW waves = HPW neighbouring KV heads of one segment.  The
+// waves stage each page together: wave w loads 256 consecutive 16-byte chunks
+// of the page's (token row x head slice) image, so the workgroup reads the
+// block's rows as long contiguous runs (2 KB per token row for 8 heads), into
+// a double-buffered tile; one barrier per page; then each wave computes its
+// own head from the tile.
+template <int G, int HPW>
+__global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
   using C = LdsCfg<G>;
+  using Tile = BlockTile<HPW>;
   constexpr int D = 128;
-  __shared__ PageTile s_tile[kWaves];
+  constexpr int kSliceChunks = HPW * 16;  // 16-byte chunks per token row of the slice
+  __shared__ Tile s_tile[2];
+  __shared__ float s_p[HPW][kPage * 8];   // softmax weights p[token][query head]
 
   const int seg = blockIdx.x;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int h = blockIdx.y * kWaves + wave;
-  if (h >= a.num_kv_heads) return;  // whole wave; the kernel has no barrier
+  const int h0 = blockIdx.y * HPW;  // first KV head of the workgroup
+  const int h = h0 + wave;
   int k = a.seg_ptr[seg];
   const int k_end = a.seg_ptr[seg + 1];
-  if (k >= k_end) return;
-  PageTile& tile = s_tile[wave];
+  if (k >= k_end) return;  // uniform over the workgroup
   const int g0 = a.pieces[k].y;
   const int n = min(a.pieces[k_end - 1].z - g0, kMaxSegPages);
+  float* p_buf = s_p[wave];
 
   // q.k role: token t, query head gq (and gq + 4 when G == 8), dim split.
   const int t = lane & 15;
   const int row = lane >> 4;
   const int gq = row % C::GP;
   const int split = row / C::GP;
-  // Staging role: load u moves tokens 4u..4u+3; lane -> (token 4u + lane/16,
-  // 16-byte chunk lane%16) of this KV head.
-  const int st_tok = lane >> 4;
-  const uint32_t st_goff = uint32_t(st_tok) * uint32_t(a.token_stride * 2) +
-                           uint32_t(h * D * 2) + uint32_t((lane & 15) * 16);
-  const uint32_t st_gstep = uint32_t(4 * a.token_stride * 2);  // bytes per load u
-  const int st_loff = st_tok * kRowPitch + (lane & 15);         // uint4 index in tile
+  // Staging role: chunk u of this lane is chunk q = 256 wave + 64 u + lane of
+  // the page image (token q / kSliceChunks, 16-byte chunk q % kSliceChunks).
+  uint32_t st_goff[4];
+  int st_loff[4], st_tok[4];
+  const uint32_t ts_bytes = uint32_t(a.token_stride * 2);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int q = 256 * wave + 64 * u + lane;
+    st_tok[u] = q / kSliceChunks;
+    const int cc = q % kSliceChunks;
+    st_goff[u] = uint32_t(st_tok[u]) * ts_bytes + uint32_t(h0 * D * 2 + cc * 16);
+    st_loff[u] = st_tok[u] * Tile::kRowChunks + cc;
+  }
   const char* kbytes = reinterpret_cast<const char*>(a.k_cache);
   const char* vbytes = reinterpret_cast<const char*>(a.v_cache);
   const int64_t block_bytes = a.block_stride * 2;
@@ -277,8 +296,8 @@ __global__ __launch_bounds__(kThreads) void decode_lds_kernel(DecodeArgs a) {
     }
   };
 
-  // A ring of kStages register stages: while page j is consumed from the LDS
-  // tile, pages j+1 .. j+kStages are in flight (kStages x 8 KB per wave).
+  // Two register stages: while page j is consumed, pages j+1 and j+2 are in
+  // flight (2 x 8 KB per wave, 2 x 8 KB x HPW per workgroup).
   struct Stage {
     uint4 k[4], v[4];
   };
@@ -288,31 +307,31 @@ __global__ __launch_bounds__(kThreads) void decode_lds_kernel(DecodeArgs a) {
     const char* vb = vbytes + int64_t(blk) * block_bytes;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      r.k[u] = *reinterpret_cast<const uint4*>(kb + u * st_gstep + st_goff);
-      r.v[u] = *reinterpret_cast<const uint4*>(vb + u * st_gstep + st_goff);
+      r.k[u] = *reinterpret_cast<const uint4*>(kb + st_goff[u]);
+      r.v[u] = *reinterpret_cast<const uint4*>(vb + st_goff[u]);
     }
   };
   auto safe_id = [&](int32_t id) { return (id >= 0 && id < a.num_blocks) ? id : 0; };
-  auto stage_tile = [&](Stage& r, int valid) {
+  auto stage_tile = [&](Stage& r, Tile& tile, int valid) {
     if (valid < kPage) {
       // Rows past the end may hold anything (even NaN bits): stage zeros so
       // that 0 * v stays 0.
 #pragma unroll
       for (int u = 0; u < 4; ++u)
-        if (4 * u + st_tok >= valid) r.k[u] = r.v[u] = make_uint4(0, 0, 0, 0);
+        if (st_tok[u] >= valid) r.k[u] = r.v[u] = make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      tile.k[st_loff + u * 4 * kRowPitch] = r.k[u];
-      tile.v[st_loff + u * 4 * kRowPitch] = r.v[u];
+      tile.k[st_loff[u]] = r.k[u];
+      tile.v[st_loff[u]] = r.v[u];
     }
   };
-  auto consume = [&](int valid) {
-    // q.k: lane (t, gq) over its chunks of K row t.
+  auto consume = [&](const Tile& tile, int valid) {
+    // q.k: lane (t, gq) over its chunks of K row t, head `wave` of the tile.
     float dots[C::QL];
 #pragma unroll
     for (int ql = 0; ql < C::QL; ++ql) dots[ql] = 0.f;
-    const uint4* krow = tile.k + t * kRowPitch + split * C::CH;
+    const uint4* krow = tile.k + t * Tile::kRowChunks + wave * 16 + split * C::CH;
 #pragma unroll
     for (int i = 0; i < C::CH; ++i) {
       const uint4 kv = krow[i];
@@ -343,7 +362,7 @@ __global__ __launch_bounds__(kThreads) void decode_lds_kernel(DecodeArgs a) {
       alpha[ql] = fast_exp2(m_run[ql] - m_new);
       l_run[ql] = fmaf(l_run[ql], alpha[ql], row16_sum(p));
       m_run[ql] = m_new;
-      if (row < C::GP) tile.p[t * G + gq + 4 * ql] = p;
+      if (row < C::GP) p_buf[t * G + gq + 4 * ql] = p;
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -354,17 +373,17 @@ __global__ __launch_bounds__(kThreads) void decode_lds_kernel(DecodeArgs a) {
     wave_lds_fence();
 
     // p.v over the 16 tokens of the page (rows past `valid` are zero).
-    const uint32_t* vcol = reinterpret_cast<const uint32_t*>(tile.v) + lane;
+    const uint32_t* vcol = reinterpret_cast<const uint32_t*>(tile.v + wave * 16) + lane;
 #pragma unroll
     for (int tt = 0; tt < kPage; ++tt) {
-      const uint32_t vw = vcol[tt * kRowPitch * 4];
+      const uint32_t vw = vcol[tt * Tile::kRowChunks * 4];
       const float v0 = bf16lo(vw);
       const float v1 = bf16hi(vw);
       float pg[G];
       if constexpr (G >= 4) {
 #pragma unroll
         for (int q4 = 0; q4 < G / 4; ++q4) {
-          const float4 x = reinterpret_cast<const float4*>(tile.p + tt * G)[q4];
+          const float4 x = reinterpret_cast<const float4*>(p_buf + tt * G)[q4];
           pg[4 * q4 + 0] = x.x;
           pg[4 * q4 + 1] = x.y;
           pg[4 * q4 + 2] = x.z;
@@ -372,7 +391,7 @@ __global__ __launch_bounds__(kThreads) void decode_lds_kernel(DecodeArgs a) {
         }
       } else {
 #pragma unroll
-        for (int g = 0; g < G; ++g) pg[g] = tile.p[tt * G + g];
+        for (int g = 0; g < G; ++g) pg[g] = p_buf[tt * G + g];
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -382,18 +401,20 @@ __global__ __launch_bounds__(kThreads) void decode_lds_kernel(DecodeArgs a) {
       if ((tt + 1) % kReadGroup == 0) __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // Page j of the segment, held in stage r (block id `id`), then the refill
-  // of r with page j+kStages and, at the end of a piece, its output.
-  auto step = [&](int j, Stage& r, int32_t& id) {
+  // Page j: stage it into tile j%2, refill its register stage with page j+2,
+  // wait for the whole workgroup's part of the tile (one barrier per page:
+  // every wave has also finished reading the tile's previous page j-2),
+  // consume, and close the piece if page j is its last.
+  auto step = [&](int j, Stage& r, int32_t& id, Tile& tile) {
     const int slot = g0 + j;
     const int valid = pc.valid(slot, id, a.num_blocks);
-    stage_tile(r, valid);
-    if (j + kStages < n) {
-      id = ids.at(j + kStages);
+    stage_tile(r, tile, valid);
+    if (j + 2 < n) {
+      id = ids.at(j + 2);
       issue(r, safe_id(id));
     }
-    wave_lds_fence();
-    consume(valid);
+    __syncthreads();
+    consume(tile, valid);
     wave_lds_fence();
     if (slot + 1 == pc.desc.z) {
       finalize();
@@ -407,17 +428,16 @@ __global__ __launch_bounds__(kThreads) void decode_lds_kernel(DecodeArgs a) {
 
   load_q(pc.desc.x);
   reset();
-  Stage ring[kStages];
-  int32_t ring_id[kStages];
-#pragma unroll
-  for (int r = 0; r < kStages; ++r) {
-    ring_id[r] = r < n ? ids.at(r) : 0;
-    if (r < n) issue(ring[r], safe_id(ring_id[r]));
+  Stage ra, rb;
+  int32_t ida = ids.at(0), idb = 0;
+  issue(ra, safe_id(ida));
+  if (n > 1) {
+    idb = ids.at(1);
+    issue(rb, safe_id(idb));
   }
-  for (int j0 = 0; j0 < n; j0 += kStages) {
-#pragma unroll
-    for (int r = 0; r < kStages; ++r)
-      if (j0 + r < n) step(j0 + r, ring[r], ring_id[r]);
+  for (int j = 0; j < n; j += 2) {
+    step(j, ra, ida, s_tile[0]);
+    if (j + 1 < n) step(j + 1, rb, idb, s_tile[1]);
   }
 }
 
@@ -697,32 +717,50 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
   if (a.lse && lane == 0) a.lse[int64_t(b) * Hq + hq] = (mx + fast_log2(S)) * kLn2;
 }
 
-template <int G, int D>
-void launch_segments(const DecodeArgs& a, int segments, int head_groups, hipStream_t s) {
-  const dim3 grid{unsigned(segments), unsigned(head_groups)};
-  if constexpr (D == 128)
-    decode_lds_kernel<G><<<grid, kThreads, 0, s>>>(a);
-  else
-    decode_reg_kernel<G, D><<<grid, kThreads, 0, s>>>(a);
+// KV heads per workgroup of the streaming kernel: 8 (one block-row slice of
+// 2 KB per token) for the head_dim-128 kernel when the heads divide evenly
+// and the register budget allows two waves per SIMD, else one; the register
+// kernel always groups 4 heads (and idles waves past the last head).
+int heads_per_workgroup(int group, int head_dim, int num_kv_heads) {
+  if (head_dim != 128) return 4;
+  return (group <= 4 && num_kv_heads % 8 == 0) ? 8 : 1;
 }
 
-template <int D>
-bool dispatch_group(int group, const DecodeArgs& a, int segments, int head_groups,
-                    hipStream_t s) {
-  switch (group) {
-    case 1: launch_segments<1, D>(a, segments, head_groups, s); return true;
-    case 2: launch_segments<2, D>(a, segments, head_groups, s); return true;
-    case 4: launch_segments<4, D>(a, segments, head_groups, s); return true;
-    case 8: launch_segments<8, D>(a, segments, head_groups, s); return true;
-    default: return false;
+// Workgroups of the streaming kernel one CU holds at once (LDS- or
+// register-limited; from the compiled kernels' resources), used to size the
+// schedule.
+int resident_workgroups_per_cu(int group, int head_dim, int hpw) {
+  if (head_dim == 128) return hpw == 8 ? 1 : (group == 8 ? 4 : 8);
+  return group <= 2 ? 2 : 1;
+}
+
+template <int G, int D>
+void launch_segments(const DecodeArgs& a, int segments, int head_groups, int hpw,
+                     hipStream_t s) {
+  const dim3 grid{unsigned(segments), unsigned(head_groups)};
+  if constexpr (D == 128) {
+    if constexpr (G <= 4) {
+      if (hpw == 8) {
+        decode_lds_kernel<G, 8><<<grid, 64 * 8, 0, s>>>(a);
+        return;
+      }
+    }
+    decode_lds_kernel<G, 1><<<grid, 64, 0, s>>>(a);
+  } else {
+    decode_reg_kernel<G, D><<<grid, kThreads, 0, s>>>(a);
   }
 }
 
-// Workgroups of the streaming kernel one CU holds at once (register-limited;
-// from the compiled kernels' VGPR counts), used to size the schedule.
-int resident_workgroups_per_cu(int group, int head_dim) {
-  if (head_dim == 128) return group <= 2 ? 3 : (group == 4 ? 2 : 1);
-  return group <= 2 ? 2 : 1;
+template <int D>
+bool dispatch_group(int group, const DecodeArgs& a, int segments, int head_groups, int hpw,
+                    hipStream_t s) {
+  switch (group) {
+    case 1: launch_segments<1, D>(a, segments, head_groups, hpw, s); return true;
+    case 2: launch_segments<2, D>(a, segments, head_groups, hpw, s); return true;
+    case 4: launch_segments<4, D>(a, segments, head_groups, hpw, s); return true;
+    case 8: launch_segments<8, D>(a, segments, head_groups, hpw, s); return true;
+    default: return false;
+  }
 }
 
 // Merge of two bf16 attention states (a8 as a standalone op).
@@ -794,7 +832,7 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, int32_t batch,
   KVC_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
               KVC_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256");
   KVC_REQUIRE(page_size == kPage, KVC_ERR_UNSUPPORTED, "page_size must be 16");
-  KVC_REQUIRE(num_kv_heads <= 65535 * kWaves, KVC_ERR_INVALID_ARG, "too many KV heads");
+  KVC_REQUIRE(num_kv_heads <= 65535, KVC_ERR_INVALID_ARG, "too many KV heads");
   KVC_REQUIRE(batch == 0 || indptr_host[0] == 0, KVC_ERR_INVALID_ARG,
               "indptr[0] must be 0");
   int32_t num_empty = 0;
@@ -804,7 +842,8 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, int32_t batch,
     num_empty += indptr_host[b + 1] == indptr_host[b];
   }
   const int64_t total = batch > 0 ? indptr_host[batch] : 0;
-  const int head_groups = (num_kv_heads + kWaves - 1) / kWaves;
+  const int hpw = heads_per_workgroup(group, head_dim, num_kv_heads);
+  const int head_groups = (num_kv_heads + hpw - 1) / hpw;
 
   // Segments per KV-head group: one resident workgroup each, at most
   // kMaxSegPages pages each, at least one page each.
@@ -814,7 +853,7 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, int32_t batch,
       segs = num_segments_hint;
     } else {
       const int64_t slots = int64_t(num_cus > 0 ? num_cus : 256) *
-                            resident_workgroups_per_cu(group, head_dim);
+                            resident_workgroups_per_cu(group, head_dim, hpw);
       segs = (slots + head_groups - 1) / head_groups;
     }
     segs = std::max<int64_t>(segs, (total + kMaxSegPages - 1) / kMaxSegPages);
@@ -829,6 +868,7 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, int32_t batch,
   sched->page_size = page_size;
   sched->num_segments = int32_t(segs);
   sched->num_head_groups = head_groups;
+  sched->heads_per_group = hpw;
   sched->total_pages = int32_t(total);
   sched->num_empty = num_empty;
   sched->plan_ints = need;
@@ -894,7 +934,9 @@ extern "C" int kvc_batch_decode_run(
   const int group = Hq / Hkv;
   KVC_REQUIRE(sched->page_size == kPage, KVC_ERR_UNSUPPORTED, "page_size must be 16");
   KVC_REQUIRE(sched->num_segments >= 0 && sched->max_partitions >= 1 &&
-                  sched->num_head_groups == (Hkv + kWaves - 1) / kWaves &&
+                  sched->heads_per_group == heads_per_workgroup(group, D, Hkv) &&
+                  sched->num_head_groups ==
+                      (Hkv + sched->heads_per_group - 1) / sched->heads_per_group &&
                   sched->plan_ints == kvc_decode_plan_ints(batch, sched->num_segments),
               KVC_ERR_INVALID_ARG, "schedule not produced by kvc_decode_plan");
   KVC_REQUIRE(num_blocks > 0 && num_indices >= sched->total_pages, KVC_ERR_INVALID_ARG,
@@ -951,9 +993,10 @@ extern "C" int kvc_batch_decode_run(
   if (sched->num_segments > 0) {
     bool launched = false;
     const int segs = sched->num_segments, hg = sched->num_head_groups;
-    if (D == 128) launched = dispatch_group<128>(group, a, segs, hg, s);
-    else if (D == 64) launched = dispatch_group<64>(group, a, segs, hg, s);
-    else if (D == 256) launched = dispatch_group<256>(group, a, segs, hg, s);
+    const int hpw = sched->heads_per_group;
+    if (D == 128) launched = dispatch_group<128>(group, a, segs, hg, hpw, s);
+    else if (D == 64) launched = dispatch_group<64>(group, a, segs, hg, hpw, s);
+    else if (D == 256) launched = dispatch_group<256>(group, a, segs, hg, hpw, s);
     KVC_REQUIRE(launched, KVC_ERR_UNSUPPORTED,
                 "unsupported (group, head_dim) = (" + std::to_string(group) + ", " +
                     std::to_string(D) + ")");

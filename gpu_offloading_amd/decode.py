@@ -114,7 +114,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
         # run, so plan() never waits for the GPU.
         lib = _lib.load()
         sched = _lib.KvcDecodeSchedule()
-        cap = lib.kvc_decode_plan_ints(batch, max(self._segments_hint, 4 * self._num_cus))
+        cap = lib.kvc_decode_plan_ints(batch, max(self._segments_hint, 8 * self._num_cus))
         for _ in range(2):
             cap4 = (cap + 3) // 4 * 4
             hs = torch.empty(cap4 + 2 * batch + 1, dtype=torch.int32, pin_memory=True)

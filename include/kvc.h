@@ -105,9 +105,9 @@ int kvc_gather_kv(
  *
  * kvc_decode_plan is host-only (no device access), like FlashInfer plan(),
  * which also reads a host indptr.  It cuts the batch's flattened page list
- * into num_segments equal segments per group of 4 KV heads (by default one
- * per workgroup the GPU holds at once; num_segments_hint > 0 forces the
- * count) and writes the plan image into plan_host:
+ * into num_segments equal segments per group of heads_per_group KV heads (by
+ * default one per workgroup the GPU holds at once; num_segments_hint > 0
+ * forces the count) and writes the plan image into plan_host:
  *   [0, num_segments]            segment -> first piece
  *   [pieces_offset, +4*pieces)   (request, first slot, end slot, partial or -1)
  *   [nparts_offset, +batch)      pieces per request
@@ -124,15 +124,15 @@ typedef struct kvc_decode_schedule {
   int32_t num_kv_heads;
   int32_t head_dim;
   int32_t page_size;
-  int32_t num_segments;     /* segments per group of 4 KV heads            */
-  int32_t num_head_groups;  /* ceil(num_kv_heads / 4)                      */
+  int32_t num_segments;     /* segments per group of KV heads              */
+  int32_t num_head_groups;  /* ceil(num_kv_heads / heads_per_group)        */
   int32_t num_pieces;
   int32_t pieces_offset;    /* int32 offsets inside the plan image         */
   int32_t nparts_offset;
   int32_t max_partitions;   /* max pieces of one request                   */
   int32_t total_pages;      /* indptr[batch]                               */
   int32_t num_empty;        /* requests with no pages (output zero)        */
-  int32_t reserved;
+  int32_t heads_per_group;  /* KV heads one workgroup streams together     */
   int64_t plan_ints;        /* int32 entries of the plan image             */
   int64_t workspace_bytes;  /* bytes kvc_batch_decode_run will use         */
 } kvc_decode_schedule;

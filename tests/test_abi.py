@@ -63,11 +63,16 @@ def _plan(lib, lens, hq=32, hkv=8, d=128, hint=0, cus=256):
     indptr = np.zeros(len(lens) + 1, np.int32)
     np.cumsum(pages, out=indptr[1:])
     sched = _lib.KvcDecodeSchedule()
-    cap = lib.kvc_decode_plan_ints(len(lens), max(hint, 4 * cus))
-    img = np.zeros(cap, np.int32)
-    st = lib.kvc_decode_plan(indptr.ctypes.data, len(lens), hq, hkv, d, 16, hint, cus,
-                             ctypes.byref(sched), img.ctypes.data, cap)
+    cap = 16
+    for _ in range(2):   # the first call reports the capacity it needs
+        img = np.zeros(cap, np.int32)
+        st = lib.kvc_decode_plan(indptr.ctypes.data, len(lens), hq, hkv, d, 16, hint, cus,
+                                 ctypes.byref(sched), img.ctypes.data, cap)
+        if st == 4:
+            assert sched.plan_ints > cap
+            cap = sched.plan_ints
     assert st == 0, lib.kvc_last_error()
+    assert sched.plan_ints == lib.kvc_decode_plan_ints(len(lens), sched.num_segments)
     return indptr, sched, img
 
 
@@ -107,14 +112,24 @@ def _check_plan_image(indptr, sched, img):
 def test_decode_plan_is_host_only_and_balanced(lib):
     lens = [1, 16, 17, 4096, 0, 300, 2049, 33]
     indptr, sched, img = _plan(lib, lens, hint=40)
-    assert sched.num_segments == 40 and sched.num_head_groups == 2
+    # 8 KV heads of head_dim 128 stream together (one workgroup per segment)
+    assert sched.num_segments == 40 and sched.num_head_groups == 1
+    assert sched.heads_per_group == 8
     assert sched.num_empty == 1
     _check_plan_image(indptr, sched, img)
     assert sched.workspace_bytes == lib.kvc_decode_workspace_bytes(
         len(lens), 32, 128, sched.max_partitions)
-    # default: one segment per resident workgroup (256 CUs x 2) per 2 head groups
+    # default: one segment per resident workgroup (256 CUs x 1 of 8 heads)
     indptr, sched, img = _plan(lib, [3000] * 64)
     assert sched.num_segments == 256
+    _check_plan_image(indptr, sched, img)
+    # KV heads that do not divide by 8 stream one per workgroup
+    indptr, sched, img = _plan(lib, [3000] * 64, hq=24, hkv=6)
+    assert sched.heads_per_group == 1 and sched.num_head_groups == 6
+    _check_plan_image(indptr, sched, img)
+    # head_dim 64 / 256 kernels group 4 heads
+    indptr, sched, img = _plan(lib, [3000] * 8, hq=32, hkv=8, d=64)
+    assert sched.heads_per_group == 4 and sched.num_head_groups == 2
     _check_plan_image(indptr, sched, img)
     # segments never exceed 256 pages, never hold less than one page
     indptr, sched, img = _plan(lib, [16 * 5000], hint=2)
