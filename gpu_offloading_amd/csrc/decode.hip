@@ -665,11 +665,15 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// One wave per (request, query head): lane p reads the log2-sum-exp of
-// partition p, the wave forms the weights, then every lane folds its D/64
-// dims over the partitions.  Requests with a single piece were finished by
-// the streaming kernel; requests with no pages get a zero output and
+// One wave per (request, query head).  The partials of the first kSpecParts
+// pieces and the log2-sum-exps are loaded together with the request's piece
+// count (all inside the max_parts rows the workspace holds for the request),
+// so the common case costs one memory round trip; lane p weighs piece p and
+// every lane folds its D/64 dims.  Requests with a single piece were finished
+// by the streaming kernel; requests with no pages get a zero output and
 // lse = -inf.
+constexpr int kSpecParts = 16;
+
 template <int D>
 __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
   constexpr int EPL = D / 64;  // dims per lane
@@ -677,17 +681,27 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
   const int b = blockIdx.y;
   const int lane = threadIdx.x;
   const int G = a.group;
-  const int nparts = min(a.req_nparts[b], a.max_parts);
-  if (nparts == 1) return;
-  uint16_t* out = a.out + int64_t(b) * a.out_stride + int64_t(hq) * D;
   const int Hq = a.num_kv_heads * G;
   const int h = hq / G;
   const int g = hq - h * G;
   const int64_t base = (int64_t(b) * a.num_kv_heads + h) * a.max_parts;
-  const float* lp = a.part_lse + base * G + g;  // partition p at lp[p * G]
+  const float* lp = a.part_lse + base * G + g;  // piece p at lp[p * G]
+  const int nparts_raw = a.req_nparts[b];
+  const int nspec = min(a.max_parts, kSpecParts);
+  const float lse_spec = lane < min(a.max_parts, 64) ? lp[int64_t(lane) * G] : -INFINITY;
+  float po[kSpecParts][EPL];
+#pragma unroll
+  for (int p = 0; p < kSpecParts; ++p) {
+    const float* src = a.part_o + ((base + p) * G + g) * D + lane * EPL;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) po[p][e] = p < nspec ? src[e] : 0.f;
+  }
+  const int nparts = min(nparts_raw, a.max_parts);
+  if (nparts == 1) return;
+  uint16_t* out = a.out + int64_t(b) * a.out_stride + int64_t(hq) * D;
 
-  float mx = -INFINITY;
-  for (int p = lane; p < nparts; p += 64) mx = fmaxf(mx, lp[int64_t(p) * G]);
+  float mx = lane < nparts ? lse_spec : -INFINITY;
+  for (int p = 64 + lane; p < nparts; p += 64) mx = fmaxf(mx, lp[int64_t(p) * G]);
   mx = wave_max(mx);
   if (nparts <= 0 || mx == -INFINITY) {
 #pragma unroll
@@ -698,16 +712,30 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
   float acc[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-  float S = 0.f;
-  for (int q0 = 0; q0 < nparts; q0 += 64) {
-    const float w = q0 + lane < nparts ? fast_exp2(lp[int64_t(q0 + lane) * G] - mx) : 0.f;
-    S += w;
-    const int cnt = min(64, nparts - q0);
-    for (int j = 0; j < cnt; ++j) {
-      const float wj = readlane_f(w, j);
-      const float* po = a.part_o + ((base + q0 + j) * G + g) * D + lane * EPL;
+  const float w0 = lane < nparts ? fast_exp2(lse_spec - mx) : 0.f;
+  float S = w0;
+  if (nparts <= kSpecParts) {
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[e] = fmaf(wj, po[e], acc[e]);
+    for (int p = 0; p < kSpecParts; ++p) {
+      if (p < nparts) {
+        const float wp = readlane_f(w0, p);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] = fmaf(wp, po[p][e], acc[e]);
+      }
+    }
+  } else {
+    for (int q0 = 0; q0 < nparts; q0 += 64) {
+      const float w = q0 == 0 ? w0
+                              : (q0 + lane < nparts
+                                     ? fast_exp2(lp[int64_t(q0 + lane) * G] - mx) : 0.f);
+      if (q0 > 0) S += w;
+      const int cnt = min(64, nparts - q0);
+      for (int j = 0; j < cnt; ++j) {
+        const float wj = readlane_f(w, j);
+        const float* src = a.part_o + ((base + q0 + j) * G + g) * D + lane * EPL;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] = fmaf(wj, src[e], acc[e]);
+      }
     }
   }
   S = wave_sum(S);

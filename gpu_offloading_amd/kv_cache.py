@@ -122,7 +122,9 @@ class PagedKVCache:
 
         self._staging_bytes = staging_bytes
         self._staging: Optional[torch.Tensor] = None
+        self._staging_free: list[Optional[torch.cuda.Event]] = [None, None]
         self._swap_stream: Optional[torch.cuda.Stream] = None
+        self._copy_stream: Optional[torch.cuda.Stream] = None
         self._pending_free: list[tuple[torch.cuda.Event, list[int], list]] = []
         self._pending_in: dict[int, torch.cuda.Event] = {}
 
@@ -289,10 +291,11 @@ class PagedKVCache:
 
     def advance(self, seq_ids: Sequence[int], num_new_tokens: Sequence[int] | int = 1) -> None:
         """``_seq_lens_cpu[sid] += n`` (and the device mirror)."""
+        lens = self._seq_lens_cpu.numpy()
         if isinstance(num_new_tokens, int):
             num_new_tokens = [num_new_tokens] * len(seq_ids)
         for sid, n in zip(seq_ids, num_new_tokens):
-            self._seq_lens_cpu[sid] += int(n)
+            lens[int(sid)] += int(n)
         self._lens_to_device()
 
     def plan_decode(self, seq_ids: Sequence[int]) -> None:
@@ -327,8 +330,7 @@ class PagedKVCache:
         self._require_gpu()
         self._sync_seqs(seq_ids)
         slots = self.slot_mapping(seq_ids, [1] * len(seq_ids), graph_n)
-        for sid in seq_ids:
-            self._seq_lens_cpu[sid] += 1
+        self._seq_lens_cpu.numpy()[np.asarray(seq_ids, dtype=np.int64)] += 1
         self._lens_to_device()
         self.plan_decode(seq_ids)
         return slots
@@ -368,14 +370,94 @@ class PagedKVCache:
 
     # ----------------------------------------------------------------- swap
     def _side_stream(self) -> torch.cuda.Stream:
+        """Stream of the swap's gather / scatter kernels."""
         if self._swap_stream is None:
             self._swap_stream = torch.cuda.Stream(device=self.device)
         return self._swap_stream
+
+    def _dma_stream(self) -> torch.cuda.Stream:
+        """Stream of the swap's host-link copies."""
+        if self._copy_stream is None:
+            self._copy_stream = torch.cuda.Stream(device=self.device)
+        return self._copy_stream
 
     def _staging_buf(self) -> torch.Tensor:
         if self._staging is None:
             self._staging = torch.empty(self._staging_bytes, dtype=torch.uint8, device=self.device)
         return self._staging
+
+    def _staging_halves(self, per_block: int):
+        """The staging buffer as two halves and the blocks one half holds."""
+        st = self._staging_buf()
+        half = st.numel() // 2 // 256 * 256
+        if half < per_block:
+            raise RuntimeError(f"staging of {st.numel()} bytes cannot hold two blocks of "
+                               f"{per_block} bytes")
+        return (st[:half], st[half:2 * half]), half // per_block
+
+    def _pipelined_swap(self, to_host: bool, ids_t: torch.Tensor, n: int,
+                        host: torch.Tensor):
+        """Move blocks ``ids_t`` of every layer between the caches and
+        ``host`` ([layers][n][2][block_bytes]) through the two staging halves:
+        gather/scatter kernels on the side stream, the host-link copies on the
+        DMA stream, ordered by events, so that the copy of one chunk overlaps
+        the kernel of the next.  A half is reused only after its previous copy
+        (swap-out) or scatter (swap-in) completed.  Returns (start, end)
+        events; the side stream has already waited for the current stream."""
+        side, dma = self._side_stream(), self._dma_stream()
+        bb = ops.block_bytes(self.k_cache[0])
+        per = 2 * bb
+        halves, chunk = self._staging_halves(per)
+        start = torch.cuda.Event(enable_timing=True)
+        (side if to_host else dma).record_event(start)
+        if not to_host:
+            dma.wait_event(start)
+        end = None
+        i = 0
+        for layer in range(self.num_layers):
+            for c0 in range(0, n, chunk):
+                c = min(chunk, n - c0)
+                b = i % 2
+                buf = halves[b][: c * per]
+                ids_c = ids_t[c0: c0 + c]
+                h0 = (layer * n + c0) * per
+                hview = host[h0: h0 + c * per]
+                done = torch.cuda.Event(enable_timing=True)
+                if to_host:
+                    if self._staging_free[b] is not None:
+                        side.wait_event(self._staging_free[b])
+                    ops.gather_blocks(self.k_cache[layer], self.v_cache[layer], ids_c, buf,
+                                      stream=side)
+                    gathered = torch.cuda.Event()
+                    gathered.record(side)
+                    dma.wait_event(gathered)
+                    with torch.cuda.stream(dma):
+                        hview.copy_(buf, non_blocking=True)
+                    done.record(dma)
+                else:
+                    if self._staging_free[b] is not None:
+                        dma.wait_event(self._staging_free[b])
+                    with torch.cuda.stream(dma):
+                        buf.copy_(hview, non_blocking=True)
+                    loaded = torch.cuda.Event()
+                    loaded.record(dma)
+                    side.wait_event(loaded)
+                    ops.scatter_blocks(buf, ids_c, self.k_cache[layer], self.v_cache[layer],
+                                       stream=side)
+                    done.record(side)
+                self._staging_free[b] = done
+                end = done
+                i += 1
+        ids_t.record_stream(side)
+        if end is None:
+            end = torch.cuda.Event(enable_timing=True)
+            end.record(side)
+        # Both streams may still be running: make the side stream (which the
+        # callers wait on) finish after the last copy too.
+        side.wait_event(end)
+        last = torch.cuda.Event(enable_timing=True)
+        last.record(side)
+        return start, last
 
     def _reclaim(self, need: int = 0) -> None:
         """Return pages of finished swap-outs to the free list; block on the
@@ -393,8 +475,9 @@ class PagedKVCache:
             self._pool.give_back(pages)
 
     def synchronize_swaps(self) -> None:
-        if self._swap_stream is not None:
-            self._swap_stream.synchronize()
+        for st in (self._swap_stream, self._copy_stream):
+            if st is not None:
+                st.synchronize()
         if self._dynamic_pages:
             self._reclaim(need=self.total_pages + 1)
 
@@ -431,15 +514,8 @@ class PagedKVCache:
         elif host.is_cuda or not host.is_pinned() or host.numel() * host.element_size() < nbytes:
             raise RuntimeError(f"host buffer must be pinned CPU memory of >= {nbytes} bytes")
         ids_t = self._to_device(np.asarray(ids, dtype=np.int32))
-        side = self._side_stream()
-        side.wait_stream(cur)
-        staging = self._staging_buf()
-        start = torch.cuda.Event(enable_timing=True)
-        start.record(side)
-        ops.swap_out_blocks(self.k_cache, self.v_cache, ids_t, host, staging, stream=side)
-        ids_t.record_stream(side)
-        ev = torch.cuda.Event(enable_timing=True)
-        ev.record(side)
+        self._side_stream().wait_stream(cur)
+        start, ev = self._pipelined_swap(True, ids_t, n, host)
         # The host buffer must outlive the D2H copy even if the handle is dropped.
         self._pending_free.append((ev, ids, [ids_t, host]))
         return SwapHandle(seq_ids, lens, npages, ids_t, host, ev, out_start=start, num_bytes=nbytes)
@@ -469,13 +545,8 @@ class PagedKVCache:
         side = self._side_stream()
         side.wait_stream(cur)
         side.wait_event(handle.out_event)
-        start = torch.cuda.Event(enable_timing=True)
-        start.record(side)
-        ops.swap_in_blocks(handle.host, dst_t, self.k_cache, self.v_cache, self._staging_buf(),
-                           stream=side)
-        dst_t.record_stream(side)
-        ev = torch.cuda.Event(enable_timing=True)
-        ev.record(side)
+        self._dma_stream().wait_stream(side)
+        start, ev = self._pipelined_swap(False, dst_t, len(dst), handle.host)
         handle.in_start = start
         self._pending_free.append((ev, [], [dst_t, handle.host]))
         handle.in_event = ev
