@@ -73,7 +73,7 @@ SIGNATURES = {
         c_int64, c_int64, _P, _P, c_int64, _I32P, _P]),
     "kvc_decode_plan_ints": (c_int64, [c_int32, c_int32]),
     "kvc_decode_plan": (c_int, [
-        c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+        c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
         POINTER(KvcDecodeSchedule), c_void_p, c_int64]),
     "kvc_decode_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32]),
     "kvc_batch_decode_run": (c_int, [

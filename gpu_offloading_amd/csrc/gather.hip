@@ -5,6 +5,8 @@
 // Design: grid (ceil(max_seq_len / kTokPerWG), batch).  A 256-thread workgroup
 // copies kTokPerWG consecutive output rows of one sequence; the work unit is a
 // 16-byte chunk of a K or V row and each lane keeps kUnroll chunks in flight.
+// Cache rows are read with non-temporal loads; 8 rows per workgroup (more
+// workgroups in flight) measured best.
 // A token row is contiguous in both the cache and the output, and rows of the
 // same block are adjacent in the cache, so loads and stores are coalesced.
 // Block (swap) gather/scatter of whole blocks lives in swap.hip.
@@ -16,7 +18,7 @@ namespace kvc {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kTokPerWG = 16;
+constexpr int kTokPerWG = 8;
 constexpr int kUnroll = 8;
 
 struct GatherArgs {
@@ -78,7 +80,7 @@ __global__ __launch_bounds__(kThreads) void gather_vec16_kernel(GatherArgs a) {
       const char* src = (is_v ? a.value_cache : a.key_cache) +
                         int64_t(blk) * a.block_stride + int64_t(off) * a.token_stride +
                         chunk * 16u;
-      buf[u] = *reinterpret_cast<const uint4*>(src);
+      buf[u] = load_stream(src);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)

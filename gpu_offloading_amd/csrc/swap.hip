@@ -57,7 +57,7 @@ __global__ __launch_bounds__(kThreads) void block_copy_kernel(BlockCopyArgs a) {
     const int64_t in_blk = is_v ? off - a.block_bytes : off;
     char* cache = (is_v ? a.value_cache : a.key_cache) + int64_t(id) * a.block_stride + in_blk;
     char* stage = a.staging + i * span + off;
-    buf[u] = *reinterpret_cast<const uint4*>(kToStaging ? cache : stage);
+    buf[u] = kToStaging ? load_stream(cache) : *reinterpret_cast<const uint4*>(stage);
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
@@ -67,7 +67,10 @@ __global__ __launch_bounds__(kThreads) void block_copy_kernel(BlockCopyArgs a) {
     const int64_t in_blk = is_v ? off - a.block_bytes : off;
     char* cache = (is_v ? a.value_cache : a.key_cache) + int64_t(id) * a.block_stride + in_blk;
     char* stage = a.staging + i * span + off;
-    *reinterpret_cast<uint4*>(kToStaging ? stage : cache) = buf[u];
+    if (kToStaging)
+      *reinterpret_cast<uint4*>(stage) = buf[u];
+    else
+      store_stream(cache, buf[u]);
   }
 }
 

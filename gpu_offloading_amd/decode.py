@@ -103,6 +103,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
 
         indptr_host = indptr[: batch + 1].to("cpu").contiguous() if indptr.is_cuda \
             else indptr[: batch + 1].contiguous()
+        lpl_host = last_page_len[:batch].to("cpu").contiguous() if last_page_len.is_cuda \
+            else last_page_len[:batch].contiguous()
         total = int(indptr_host[-1]) if batch > 0 else 0
         if indices.numel() < total:
             _fail(f"indices has {indices.numel()} entries, indptr[-1] = {total}")
@@ -118,7 +120,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
         for _ in range(2):
             cap4 = (cap + 3) // 4 * 4
             hs = torch.empty(cap4 + 2 * batch + 1, dtype=torch.int32, pin_memory=True)
-            st = lib.kvc_decode_plan(indptr_host.data_ptr(), batch, num_qo_heads, num_kv_heads,
+            st = lib.kvc_decode_plan(indptr_host.data_ptr(), lpl_host.data_ptr(), batch,
+                                     num_qo_heads, num_kv_heads,
                                      head_dim, page_size, self._segments_hint, self._num_cus,
                                      sched, hs.data_ptr(), cap4)
             if st == _lib.KVC_ERR_WORKSPACE and sched.plan_ints > cap4:
@@ -132,7 +135,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
 
         dev = self._device
         hs[cap4: cap4 + batch + 1].copy_(indptr_host)
-        hs[cap4 + batch + 1:].copy_(last_page_len[:batch])
+        hs[cap4 + batch + 1:].copy_(lpl_host)
         dm = hs.to(dev, non_blocking=True)
         plan_dev = dm[:cap4]
         if self._indptr_buf is not None:

@@ -108,9 +108,12 @@ int kvc_gather_kv(
  * into num_segments equal segments per group of heads_per_group KV heads (by
  * default one per workgroup the GPU holds at once; num_segments_hint > 0
  * forces the count) and writes the plan image into plan_host:
- *   [0, num_segments]            segment -> first piece
- *   [pieces_offset, +4*pieces)   (request, first slot, end slot, partial or -1)
+ *   [0, 4*num_segments)          (first piece, end piece, first slot, pages)
+ *   [pieces_offset, +8*pieces)   (request, first slot, end slot, partial or -1,
+ *                                 request's last slot, its tokens, 0, 0)
  *   [nparts_offset, +batch)      pieces per request
+ * last_page_len_host (tokens in each request's final page) is copied into
+ * the pieces so that the kernel needs no dependent load at a piece switch.
  * (plan_ints int32 in total; kvc_decode_plan_ints gives the size for a
  * segment count).  If plan_capacity is too small it fills schedule->plan_ints
  * and returns KVC_ERR_WORKSPACE.  The caller copies the image to the device
@@ -139,8 +142,8 @@ typedef struct kvc_decode_schedule {
 
 int64_t kvc_decode_plan_ints(int32_t batch, int32_t num_segments);
 
-int kvc_decode_plan(const int32_t* indptr_host, int32_t batch,
-                    int32_t num_qo_heads, int32_t num_kv_heads,
+int kvc_decode_plan(const int32_t* indptr_host, const int32_t* last_page_len_host,
+                    int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
                     int32_t head_dim, int32_t page_size,
                     int32_t num_segments_hint, int32_t num_cus,
                     kvc_decode_schedule* schedule, int32_t* plan_host,

@@ -59,41 +59,50 @@ def test_version_and_status_strings(lib):
 
 
 def _plan(lib, lens, hq=32, hkv=8, d=128, hint=0, cus=256):
-    pages = (np.asarray(lens, np.int64) + 15) // 16
+    lens = np.asarray(lens, np.int64)
+    pages = (lens + 15) // 16
     indptr = np.zeros(len(lens) + 1, np.int32)
     np.cumsum(pages, out=indptr[1:])
+    lpl = np.where((lens % 16 == 0) & (lens > 0), 16, lens % 16).astype(np.int32)
     sched = _lib.KvcDecodeSchedule()
     cap = 16
     for _ in range(2):   # the first call reports the capacity it needs
         img = np.zeros(cap, np.int32)
-        st = lib.kvc_decode_plan(indptr.ctypes.data, len(lens), hq, hkv, d, 16, hint, cus,
-                                 ctypes.byref(sched), img.ctypes.data, cap)
+        st = lib.kvc_decode_plan(indptr.ctypes.data, lpl.ctypes.data, len(lens), hq, hkv, d,
+                                 16, hint, cus, ctypes.byref(sched), img.ctypes.data, cap)
         if st == 4:
             assert sched.plan_ints > cap
             cap = sched.plan_ints
     assert st == 0, lib.kvc_last_error()
     assert sched.plan_ints == lib.kvc_decode_plan_ints(len(lens), sched.num_segments)
-    return indptr, sched, img
+    return indptr, sched, img, lpl
 
 
-def _check_plan_image(indptr, sched, img):
+def _check_plan_image(indptr, sched, img, lpl):
     """Segments are contiguous, equal to within one page, at most 256 pages,
     and their pieces tile every request's pages exactly once, numbered
-    0..n-1 per request (-1 when a request is a single piece)."""
+    0..n-1 per request (-1 when a request is a single piece), each carrying
+    its request's last slot and last-page length."""
     S = sched.num_segments
-    seg_ptr = img[:S + 1]
-    pieces = img[sched.pieces_offset:sched.pieces_offset + 4 * sched.num_pieces].reshape(-1, 4)
+    segs = img[:4 * S].reshape(-1, 4)
+    rec = img[sched.pieces_offset:sched.pieces_offset + 8 * sched.num_pieces].reshape(-1, 8)
+    pieces = rec[:, :4]
     nparts = img[sched.nparts_offset:sched.nparts_offset + sched.batch]
     total = int(indptr[-1])
-    assert sched.total_pages == total and seg_ptr[0] == 0 and seg_ptr[-1] == sched.num_pieces
+    assert sched.total_pages == total
+    assert segs[0, 0] == 0 and segs[-1, 1] == sched.num_pieces
+    assert (segs[1:, 0] == segs[:-1, 1]).all()
     lengths = []
     for s in range(S):
-        ps = pieces[seg_ptr[s]:seg_ptr[s + 1]]
+        ps = pieces[segs[s, 0]:segs[s, 1]]
         assert len(ps) >= 1
         assert (ps[1:, 1] == ps[:-1, 2]).all()                 # contiguous slots
         assert ps[0, 1] == s * total // S and ps[-1, 2] == (s + 1) * total // S
+        assert segs[s, 2] == ps[0, 1] and segs[s, 3] == ps[-1, 2] - ps[0, 1]
         lengths.append(ps[-1, 2] - ps[0, 1])
     assert max(lengths) - min(lengths) <= 1 and max(lengths) <= 256
+    assert (rec[:, 4] == indptr[rec[:, 0] + 1] - 1).all()
+    assert (rec[:, 5] == lpl[rec[:, 0]]).all()
     for b in range(sched.batch):
         mine = pieces[pieces[:, 0] == b]
         assert len(mine) == nparts[b]
@@ -111,33 +120,33 @@ def _check_plan_image(indptr, sched, img):
 
 def test_decode_plan_is_host_only_and_balanced(lib):
     lens = [1, 16, 17, 4096, 0, 300, 2049, 33]
-    indptr, sched, img = _plan(lib, lens, hint=40)
+    indptr, sched, img, lpl = _plan(lib, lens, hint=40)
     # 8 KV heads of head_dim 128 stream together (one workgroup per segment)
     assert sched.num_segments == 40 and sched.num_head_groups == 1
     assert sched.heads_per_group == 8
     assert sched.num_empty == 1
-    _check_plan_image(indptr, sched, img)
+    _check_plan_image(indptr, sched, img, lpl)
     assert sched.workspace_bytes == lib.kvc_decode_workspace_bytes(
         len(lens), 32, 128, sched.max_partitions)
     # default: one segment per resident workgroup (256 CUs x 1 of 8 heads)
-    indptr, sched, img = _plan(lib, [3000] * 64)
+    indptr, sched, img, lpl = _plan(lib, [3000] * 64)
     assert sched.num_segments == 256
-    _check_plan_image(indptr, sched, img)
+    _check_plan_image(indptr, sched, img, lpl)
     # KV heads that do not divide by 8 stream one per workgroup
-    indptr, sched, img = _plan(lib, [3000] * 64, hq=24, hkv=6)
+    indptr, sched, img, lpl = _plan(lib, [3000] * 64, hq=24, hkv=6)
     assert sched.heads_per_group == 1 and sched.num_head_groups == 6
-    _check_plan_image(indptr, sched, img)
+    _check_plan_image(indptr, sched, img, lpl)
     # head_dim 64 / 256 kernels group 4 heads
-    indptr, sched, img = _plan(lib, [3000] * 8, hq=32, hkv=8, d=64)
+    indptr, sched, img, lpl = _plan(lib, [3000] * 8, hq=32, hkv=8, d=64)
     assert sched.heads_per_group == 4 and sched.num_head_groups == 2
-    _check_plan_image(indptr, sched, img)
+    _check_plan_image(indptr, sched, img, lpl)
     # segments never exceed 256 pages, never hold less than one page
-    indptr, sched, img = _plan(lib, [16 * 5000], hint=2)
+    indptr, sched, img, lpl = _plan(lib, [16 * 5000], hint=2)
     assert sched.num_segments == 20
-    _check_plan_image(indptr, sched, img)
-    indptr, sched, img = _plan(lib, [40, 1], hint=1000)
+    _check_plan_image(indptr, sched, img, lpl)
+    indptr, sched, img, lpl = _plan(lib, [40, 1], hint=1000)
     assert sched.num_segments == 4
-    _check_plan_image(indptr, sched, img)
+    _check_plan_image(indptr, sched, img, lpl)
 
 
 def test_decode_plan_random_batches(lib):
@@ -146,20 +155,21 @@ def test_decode_plan_random_batches(lib):
         lens = rng.integers(0, 3000, rng.integers(1, 80)).tolist()
         hkv = int(rng.choice([1, 4, 8, 16]))
         hint = int(rng.choice([0, 1, 7, 64, 333]))
-        indptr, sched, img = _plan(lib, lens, hq=hkv * 4, hkv=hkv, hint=hint,
+        indptr, sched, img, lpl = _plan(lib, lens, hq=hkv * 4, hkv=hkv, hint=hint,
                                    cus=int(rng.integers(1, 300)))
         if indptr[-1] == 0:
             assert sched.num_segments == 0
             continue
-        _check_plan_image(indptr, sched, img)
+        _check_plan_image(indptr, sched, img, lpl)
 
 
 def test_decode_plan_reports_the_needed_capacity(lib):
     indptr = np.array([0, 100, 100, 300], np.int32)
+    lpl = np.array([16, 0, 16], np.int32)
     sched = _lib.KvcDecodeSchedule()
     small = np.zeros(4, np.int32)
-    st = lib.kvc_decode_plan(indptr.ctypes.data, 3, 32, 8, 128, 16, 50, 256, ctypes.byref(sched),
-                             small.ctypes.data, 4)
+    st = lib.kvc_decode_plan(indptr.ctypes.data, lpl.ctypes.data, 3, 32, 8, 128, 16, 50, 256,
+                             ctypes.byref(sched), small.ctypes.data, 4)
     assert st == 4 and sched.plan_ints == lib.kvc_decode_plan_ints(3, 50)
     assert b"plan buffer too small" in lib.kvc_last_error()
 
@@ -169,8 +179,10 @@ def test_decode_plan_rejects_bad_shapes(lib):
     sched = _lib.KvcDecodeSchedule()
     img = np.zeros(4096, np.int32)
 
+    lpl = np.full(4, 16, np.int32)
+
     def plan(hq, hkv, d, ps, ip=indptr, batch=1):
-        return lib.kvc_decode_plan(ip.ctypes.data, batch, hq, hkv, d, ps, 0, 256,
+        return lib.kvc_decode_plan(ip.ctypes.data, lpl.ctypes.data, batch, hq, hkv, d, ps, 0, 256,
                                    ctypes.byref(sched), img.ctypes.data, img.size)
 
     assert plan(12, 8, 128, 16) == 1
