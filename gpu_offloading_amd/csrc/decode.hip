@@ -39,9 +39,11 @@
 //   p.v : lane l owns dims 2l, 2l+1 for every query head; per token one
 //         ds_read_b32 of V and one broadcast read of p[t][0..G).
 // Softmax statistics live per 16-lane DPP row (one query head per row).
-// A wave's page ids are loaded once, one per lane (4 registers: up to 256
-// pages), and broadcast with v_readlane, so no dependent global load sits in
-// the streaming loop.
+// A wave's page ids are loaded once, one per lane (2 registers: up to 128
+// pages per segment), and broadcast with v_readlane, so no dependent global
+// load sits in the streaming loop.  A workgroup derives its span of the page
+// list from its segment index, so the id loads and the segment/piece record
+// loads go out together at kernel start.
 //
 // head_dim 64 and 256 use decode_reg_kernel: grid (S, ceil(Hkv / 4)), one
 // wave per KV head, no barrier; K/V stay in registers: lane (row r, column c)
@@ -59,7 +61,7 @@ constexpr int kThreads = 256;          // register kernel workgroup
 constexpr int kWaves = kThreads / 64;  // KV heads per register-kernel workgroup
 constexpr int kPage = 16;              // tokens per page (the engine's page_size)
 constexpr int kTokPerRow = 4;          // register kernel: tokens of a page per 16-lane row
-constexpr int kIdRegs = 4;             // page-id registers per lane
+constexpr int kIdRegs = 2;             // page-id registers per lane
 constexpr int kMaxSegPages = 64 * kIdRegs;
 constexpr int kReadGroup = 4;  // LDS reads scheduled together
 constexpr int kStages = 2;  // pages in flight per wave (LDS kernel)
@@ -81,6 +83,8 @@ struct DecodeArgs {
   int64_t num_indices;
   const int32_t* last_page_len;
   const int4* segments;    // [S]: (first piece, end piece, first slot, pages)
+  int32_t total_pages;     // pages of the whole batch
+  int32_t num_segments;
   const int4* pieces;      // [N][2]: (request, first slot, end slot, partial or -1),
                            //         (request's last slot, its tokens, 0, 0)
   float scale_log2;        // sm_scale * log2(e)
@@ -113,25 +117,46 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// First slot and page count of segment s.  The plan cuts the flattened page
+// list into equal parts, so both follow from the segment index, and a
+// workgroup can fetch its page ids without waiting for its segment record.
+__device__ __forceinline__ void segment_span(const DecodeArgs& a, int s, int& g0, int& n) {
+  const int64_t t = a.total_pages;
+  g0 = int(int64_t(s) * t / a.num_segments);
+  n = min(int(int64_t(s + 1) * t / a.num_segments) - g0, kMaxSegPages);
+}
+
 // Page ids of a segment: lane l of register r holds indices[g0 + l + 64 r].
+// The registers are only ever indexed by constants (v_readlane picks the
+// lane): a runtime index would turn them into a per-thread LDS array.
 struct SegmentIds {
   int32_t r[kIdRegs];
 
   __device__ __forceinline__ void load(const DecodeArgs& a, int g0, int n, int lane) {
+    // Clamped addresses, uniform branches: the loads issue back to back.
+    const int64_t last = a.num_indices - 1;
 #pragma unroll
     for (int i = 0; i < kIdRegs; ++i) {
-      const int j = lane + 64 * i;
-      const int64_t slot = int64_t(g0) + j;
-      r[i] = (j < n && slot < a.num_indices) ? a.indices[slot] : -1;
+      r[i] = -1;
+      if (64 * i < n) {
+        const int j = lane + 64 * i;
+        const int64_t slot = int64_t(g0) + j;
+        const int32_t v = a.indices[min(slot, last)];
+        r[i] = (j < n && slot <= last) ? v : -1;
+      }
     }
   }
   // Block id of the segment's j-th page (j uniform).
   __device__ __forceinline__ int32_t at(int j) const {
+    const int l = j & 63;
     const int w = j >> 6;
-    int32_t v = r[0];
+    int32_t v = __builtin_amdgcn_readlane(r[0], l);
 #pragma unroll
-    for (int i = 1; i < kIdRegs; ++i) v = w == i ? r[i] : v;
-    return __builtin_amdgcn_readlane(v, j & 63);
+    for (int i = 1; i < kIdRegs; ++i) {
+      const int32_t x = __builtin_amdgcn_readlane(r[i], l);
+      v = w == i ? x : v;
+    }
+    return v;
   }
 };
 
@@ -227,10 +252,10 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
   const int h0 = blockIdx.y * HPW;  // first KV head of the workgroup
   const int h = h0 + wave;
   const int4 segment = a.segments[blockIdx.x];
+  int g0, n;
+  segment_span(a, blockIdx.x, g0, n);
   int k = segment.x;
   const int k_end = segment.y;
-  const int g0 = segment.z;
-  const int n = min(segment.w, kMaxSegPages);
   if (k >= k_end || n <= 0) return;  // uniform over the workgroup
   float* p_buf = s_p[wave];
 
@@ -262,7 +287,7 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
   pc.load(a, k);
 
   uint32_t qw[C::QL][C::CH * 4];
-  auto load_q = [&](int b) {
+  auto load_q = [&](int b) __attribute__((always_inline)) {
 #pragma unroll
     for (int ql = 0; ql < C::QL; ++ql) {
       const uint4* qp = reinterpret_cast<const uint4*>(
@@ -278,7 +303,7 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
     }
   };
   float m_run[C::QL], l_run[C::QL], acc[G][2];
-  auto reset = [&]() {
+  auto reset = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int ql = 0; ql < C::QL; ++ql) {
       m_run[ql] = kNegBig;
@@ -287,7 +312,7 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
   };
-  auto finalize = [&]() {
+  auto finalize = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const float l = readlane_f(l_run[g / 4], 16 * (g % 4));
@@ -304,7 +329,7 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
   struct Stage {
     uint4 k[4], v[4];
   };
-  auto issue = [&](Stage& r, int32_t blk) {
+  auto issue = [&](Stage& r, int32_t blk) __attribute__((always_inline)) {
     // Uniform block base (SGPRs) + 32-bit lane offset.
     const char* kb = kbytes + int64_t(blk) * block_bytes;
     const char* vb = vbytes + int64_t(blk) * block_bytes;
@@ -314,8 +339,8 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
       r.v[u] = load_stream(vb + st_goff[u]);
     }
   };
-  auto safe_id = [&](int32_t id) { return (id >= 0 && id < a.num_blocks) ? id : 0; };
-  auto stage_tile = [&](Stage& r, Tile& tile, int valid) {
+  auto safe_id = [&](int32_t id) __attribute__((always_inline)) { return (id >= 0 && id < a.num_blocks) ? id : 0; };
+  auto stage_tile = [&](Stage& r, Tile& tile, int valid) __attribute__((always_inline)) {
     if (valid < kPage) {
       // Rows past the end may hold anything (even NaN bits): stage zeros so
       // that 0 * v stays 0.
@@ -329,7 +354,7 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
       tile.v[st_loff[u]] = r.v[u];
     }
   };
-  auto consume = [&](const Tile& tile, int valid) {
+  auto consume = [&](const Tile& tile, int valid) __attribute__((always_inline)) {
     // q.k: lane (t, gq) over its chunks of K row t, head `wave` of the tile.
     float dots[C::QL];
 #pragma unroll
@@ -408,7 +433,7 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
   // wait for the whole workgroup's part of the tile (one barrier per page:
   // every wave has also finished reading the tile's previous page j-2),
   // consume, and close the piece if page j is its last.
-  auto step = [&](int j, Stage& r, int32_t& id, Tile& tile) {
+  auto step = [&](int j, Stage& r, int32_t& id, Tile& tile) __attribute__((always_inline)) {
     const int slot = g0 + j;
     const int valid = pc.valid(slot, id, a.num_blocks);
     stage_tile(r, tile, valid);
@@ -548,10 +573,10 @@ __global__ __launch_bounds__(kThreads) void decode_reg_kernel(DecodeArgs a) {
   const int h = blockIdx.y * kWaves + wave;
   if (h >= a.num_kv_heads) return;
   const int4 segment = a.segments[blockIdx.x];
+  int g0, n;
+  segment_span(a, blockIdx.x, g0, n);
   int k = segment.x;
   const int k_end = segment.y;
-  const int g0 = segment.z;
-  const int n = min(segment.w, kMaxSegPages);
   if (k >= k_end || n <= 0) return;
   const int row = lane >> 4;
   const int col = lane & 15;
@@ -563,13 +588,13 @@ __global__ __launch_bounds__(kThreads) void decode_reg_kernel(DecodeArgs a) {
   pc.load(a, k);
 
   uint32_t qw[G][W];
-  auto load_q = [&](int b) {
+  auto load_q = [&](int b) __attribute__((always_inline)) {
     const uint16_t* qb = a.q + int64_t(b) * a.q_stride + int64_t(h) * G * D + col * E;
 #pragma unroll
     for (int g = 0; g < G; ++g) load_slice<D>(qw[g], qb + g * D);
   };
   float m[G], l[G], acc[G][E];
-  auto reset = [&]() {
+  auto reset = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       m[g] = kNegBig;
@@ -578,7 +603,7 @@ __global__ __launch_bounds__(kThreads) void decode_reg_kernel(DecodeArgs a) {
       for (int e = 0; e < E; ++e) acc[g][e] = 0.f;
     }
   };
-  auto finalize = [&]() {
+  auto finalize = [&]() __attribute__((always_inline)) {
     // Merge the four rows (lanes c, c+16, c+32, c+48 hold the same dims).
 #pragma unroll
     for (int off = 16; off <= 32; off <<= 1) {
@@ -612,9 +637,9 @@ __global__ __launch_bounds__(kThreads) void decode_reg_kernel(DecodeArgs a) {
   };
 
   // Two register sets: page j is consumed while page j+1 is in flight.
-  auto safe = [&](int32_t id) { return (id >= 0 && id < a.num_blocks) ? id : 0; };
+  auto safe = [&](int32_t id) __attribute__((always_inline)) { return (id >= 0 && id < a.num_blocks) ? id : 0; };
   PageRegs<D> ra, rb;
-  auto step = [&](int j, PageRegs<D>& cur, int32_t id, PageRegs<D>& nxt, int32_t& nid) {
+  auto step = [&](int j, PageRegs<D>& cur, int32_t id, PageRegs<D>& nxt, int32_t& nid) __attribute__((always_inline)) {
     const int slot = g0 + j;
     if (j + 1 < n) {
       nid = ids.at(j + 1);
@@ -879,17 +904,20 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, const int32_t* last_p
   const int head_groups = (num_kv_heads + hpw - 1) / hpw;
 
   // Segments per KV-head group: one resident workgroup each, at most
-  // kMaxSegPages pages each, at least one page each.
+  // kMaxSegPages pages each, at least one page each.  When the page cap
+  // forces more segments than there are resident slots, the count is rounded
+  // up to whole rounds of slots, so no round runs a few stragglers alone.
   int64_t segs = 0;
   if (total > 0) {
+    const int64_t at_least = (total + kMaxSegPages - 1) / kMaxSegPages;
     if (num_segments_hint > 0) {
-      segs = num_segments_hint;
+      segs = std::max<int64_t>(num_segments_hint, at_least);
     } else {
       const int64_t slots = int64_t(num_cus > 0 ? num_cus : 256) *
                             resident_workgroups_per_cu(group, head_dim, hpw);
-      segs = (slots + head_groups - 1) / head_groups;
+      const int64_t per_round = (slots + head_groups - 1) / head_groups;
+      segs = (std::max(per_round, at_least) + per_round - 1) / per_round * per_round;
     }
-    segs = std::max<int64_t>(segs, (total + kMaxSegPages - 1) / kMaxSegPages);
     segs = std::min<int64_t>(segs, total);
   }
   KVC_REQUIRE(segs <= (int64_t(1) << 30), KVC_ERR_INVALID_ARG, "too many segments");
@@ -1017,6 +1045,8 @@ extern "C" int kvc_batch_decode_run(
   a.last_page_len = last_page_len;
   a.segments = reinterpret_cast<const int4*>(plan);
   a.pieces = reinterpret_cast<const int4*>(plan + sched->pieces_offset);
+  a.total_pages = sched->total_pages;
+  a.num_segments = sched->num_segments;
   a.scale_log2 = sm_scale * kLog2e;
   a.num_kv_heads = Hkv;
   a.max_parts = sched->max_partitions;

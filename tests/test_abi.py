@@ -79,7 +79,7 @@ def _plan(lib, lens, hq=32, hkv=8, d=128, hint=0, cus=256):
 
 
 def _check_plan_image(indptr, sched, img, lpl):
-    """Segments are contiguous, equal to within one page, at most 256 pages,
+    """Segments are contiguous, equal to within one page, at most 128 pages,
     and their pieces tile every request's pages exactly once, numbered
     0..n-1 per request (-1 when a request is a single piece), each carrying
     its request's last slot and last-page length."""
@@ -100,7 +100,7 @@ def _check_plan_image(indptr, sched, img, lpl):
         assert ps[0, 1] == s * total // S and ps[-1, 2] == (s + 1) * total // S
         assert segs[s, 2] == ps[0, 1] and segs[s, 3] == ps[-1, 2] - ps[0, 1]
         lengths.append(ps[-1, 2] - ps[0, 1])
-    assert max(lengths) - min(lengths) <= 1 and max(lengths) <= 256
+    assert max(lengths) - min(lengths) <= 1 and max(lengths) <= 128
     assert (rec[:, 4] == indptr[rec[:, 0] + 1] - 1).all()
     assert (rec[:, 5] == lpl[rec[:, 0]]).all()
     for b in range(sched.batch):
@@ -140,9 +140,17 @@ def test_decode_plan_is_host_only_and_balanced(lib):
     indptr, sched, img, lpl = _plan(lib, [3000] * 8, hq=32, hkv=8, d=64)
     assert sched.heads_per_group == 4 and sched.num_head_groups == 2
     _check_plan_image(indptr, sched, img, lpl)
-    # segments never exceed 256 pages, never hold less than one page
+    # segments never exceed 128 pages, never hold less than one page
     indptr, sched, img, lpl = _plan(lib, [16 * 5000], hint=2)
-    assert sched.num_segments == 20
+    assert sched.num_segments == 40
+    _check_plan_image(indptr, sched, img, lpl)
+    # past 128 pages per resident slot, whole rounds of slots: 40000 pages
+    # need 313 segments, rounded up to 2 x 256
+    indptr, sched, img, lpl = _plan(lib, [16 * 20000] * 2)
+    assert sched.num_segments == 512
+    _check_plan_image(indptr, sched, img, lpl)
+    indptr, sched, img, lpl = _plan(lib, [16 * 20000] * 2, cus=100)
+    assert sched.num_segments == 400
     _check_plan_image(indptr, sched, img, lpl)
     indptr, sched, img, lpl = _plan(lib, [40, 1], hint=1000)
     assert sched.num_segments == 4

@@ -113,7 +113,7 @@ def test_decode_segment_counts_agree(gpu, segs):
                          segs=segs)
     if segs is not None:
         total = int(indptr[-1])
-        assert w.schedule.num_segments == min(max(segs, (total + 255) // 256), total)
+        assert w.schedule.num_segments == min(max(segs, (total + 127) // 128), total)
     ref, ref_lse = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
     assert_attn_close(out.float().cpu().numpy(), ref)
     assert np.allclose(lse.cpu().numpy(), ref_lse, atol=1e-3, rtol=1e-4)
