@@ -54,6 +54,24 @@ class KvcDecodeSchedule(ctypes.Structure):
     ]
 
 
+class KvcPrefillSchedule(ctypes.Structure):
+    """Mirror of ``kvc_prefill_schedule`` (include/kvc.h)."""
+
+    _fields_ = [
+        ("batch", c_int32),
+        ("num_qo_heads", c_int32),
+        ("num_kv_heads", c_int32),
+        ("head_dim", c_int32),
+        ("page_size", c_int32),
+        ("causal", c_int32),
+        ("tile_tokens", c_int32),
+        ("num_items", c_int32),
+        ("total_q", c_int32),
+        ("max_key_tiles", c_int32),
+        ("plan_ints", c_int64),
+    ]
+
+
 _P = c_void_p
 _I32P = c_void_p  # device int32 pointers are passed as raw addresses
 # name -> (restype, argtypes).  Every entry point of include/kvc.h is listed;
@@ -79,6 +97,12 @@ SIGNATURES = {
     "kvc_batch_decode_run": (c_int, [
         POINTER(KvcDecodeSchedule), _I32P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64,
         _I32P, _I32P, c_int64, _I32P, c_float, _P, c_int64, _P, c_int64, _P, _P]),
+    "kvc_prefill_plan": (c_int, [
+        c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+        POINTER(KvcPrefillSchedule), c_void_p, c_int64]),
+    "kvc_batch_prefill_run": (c_int, [
+        POINTER(KvcPrefillSchedule), _I32P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64,
+        _I32P, c_int64, c_float, _P, c_int64, _P, _P]),
     "kvc_merge_attention_states": (c_int, [
         _P, _P, _P, _P, c_int64, c_int32, _P, _P, _P]),
     "kvc_gather_blocks": (c_int, [

@@ -166,6 +166,62 @@ int kvc_batch_decode_run(
     void* out, int64_t out_batch_stride, float* lse, void* stream);
 
 /* ------------------------------------------------------------------------
+ * (f2) Paged-KV prefill attention: multi-token queries over the paged cache
+ * (bf16 in/out, fp32 accumulate, MFMA).  Replaces FlashInfer
+ * BatchPrefillWithPagedKVCacheWrapper.plan/run as called for continuation
+ * prefills at src/MoE/moe_engine.py:1733-1751, :3710-3727 (plan) and
+ * :3939-3941 (run).
+ * Request b's queries are rows qo_indptr[b] .. qo_indptr[b+1] of q (q_len
+ * tokens) and its keys the kv_len tokens of pages
+ * indices[kv_indptr[b] .. kv_indptr[b+1]) (the final page holding
+ * last_page_len[b] tokens).  Query i (0-based in the request) sees key j when
+ * j <= i + kv_len - q_len (causal, aligned to the end of the cache, as
+ * FlashInfer) or always (causal = 0):
+ *   out[qo_indptr[b]+i][hq] = softmax_j(sm_scale q.K[j][hq/group]) . V[j][hq/group]
+ * A query that sees no key gets 0 (lse -inf).  Optional lse[row][hq] is the
+ * natural-log log-sum-exp of the scaled logits.
+ *
+ * kvc_prefill_plan is host-only: it cuts every request's queries into tiles
+ * of tile_tokens tokens (128 query rows = tile_tokens x group heads) and
+ * orders them longest-first.  The plan image is num_items records of 8 int32:
+ *   (request, first query, q_len, kv_len, qo_indptr[b], kv_indptr[b],
+ *    64-key tiles to visit, pages)
+ * If plan_capacity is too small it fills schedule->plan_ints and returns
+ * KVC_ERR_WORKSPACE.  The caller copies the image (16-byte aligned) to the
+ * device for kvc_batch_prefill_run.  head_dim 128, page_size 16,
+ * group 1/2/4/8.
+ * ---------------------------------------------------------------------- */
+typedef struct kvc_prefill_schedule {
+  int32_t batch;
+  int32_t num_qo_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t page_size;
+  int32_t causal;
+  int32_t tile_tokens;      /* query tokens per work item                  */
+  int32_t num_items;        /* work items per KV head                      */
+  int32_t total_q;          /* qo_indptr[batch]                            */
+  int32_t max_key_tiles;    /* most 64-key tiles one item visits           */
+  int64_t plan_ints;        /* int32 entries of the plan image             */
+} kvc_prefill_schedule;
+
+int kvc_prefill_plan(const int32_t* qo_indptr_host, const int32_t* kv_indptr_host,
+                     const int32_t* last_page_len_host, int32_t batch,
+                     int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                     int32_t page_size, int32_t causal,
+                     kvc_prefill_schedule* schedule, int32_t* plan_host,
+                     int64_t plan_capacity);
+
+/* q/out: [total_q][num_qo_heads][head_dim] with a token stride (elements). */
+int kvc_batch_prefill_run(
+    const kvc_prefill_schedule* schedule, const int32_t* plan,
+    const void* q, int64_t q_token_stride,
+    const void* key_cache, const void* value_cache,
+    int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t num_blocks, const int32_t* indices, int64_t num_indices,
+    float sm_scale, void* out, int64_t out_token_stride, float* lse, void* stream);
+
+/* ------------------------------------------------------------------------
  * (a8) Merge two attention states, fp32 math:
  *   lse = logaddexp(lse1, lse2); out = out1*e^(lse1-lse) + out2*e^(lse2-lse)
  * Restates src/dense/offload_kv_attn.py:24-39 on the device.  out* are bf16

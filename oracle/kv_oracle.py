@@ -235,6 +235,55 @@ def paged_decode(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
     return out, lse
 
 
+def paged_prefill(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+                  qo_indptr: np.ndarray, kv_indptr: np.ndarray, indices: np.ndarray,
+                  last_page_len: np.ndarray, causal: bool = True,
+                  sm_scale: Optional[float] = None):
+    """fp32 naive paged prefill attention, the semantics of FlashInfer
+    BatchPrefillWithPagedKVCacheWrapper.run as the engine calls it for
+    continuation prefills (moe_engine.py:3939-3941; plan :3710-3727 with
+    causal=True, pos_encoding_mode "NONE", default sm_scale 1/sqrt(head_dim)).
+    Request b owns query rows qo_indptr[b]..qo_indptr[b+1] (q_len) and the
+    kv_len = (pages-1)*ps + last_page_len[b] cached tokens of its pages; with
+    causal masking query i sees keys j <= i + kv_len - q_len (the chunk is
+    the tail of the cache).  A query that sees nothing gives out 0, lse -inf.
+    q: bf16 bits [total_q, Hq, D]; returns (out float32, lse float32 natural log)."""
+    q = bf16_to_f32(q)
+    T, Hq, D = q.shape
+    nb, ps, Hkv, _ = k_cache.shape
+    G = Hq // Hkv
+    scale = np.float32(1.0 / np.sqrt(D) if sm_scale is None else sm_scale)
+    out = np.zeros((T, Hq, D), np.float32)
+    lse = np.full((T, Hq), -np.inf, np.float32)
+    for b in range(len(qo_indptr) - 1):
+        q0, q1 = int(qo_indptr[b]), int(qo_indptr[b + 1])
+        pages = indices[kv_indptr[b]:kv_indptr[b + 1]]
+        if q1 == q0 or len(pages) == 0:
+            continue
+        q_len = q1 - q0
+        n = (len(pages) - 1) * ps + int(last_page_len[b])
+        K = bf16_to_f32(k_cache[pages].reshape(-1, Hkv, D)[:n])
+        V = bf16_to_f32(v_cache[pages].reshape(-1, Hkv, D)[:n])
+        seen = np.ones((q_len, n), bool)
+        if causal:
+            seen = np.arange(n)[None, :] <= np.arange(q_len)[:, None] + (n - q_len)
+        any_seen = seen.any(axis=1)
+        for h in range(Hkv):
+            for g in range(G):
+                hq = h * G + g
+                s = (q[q0:q1, hq] @ K[:, h, :].T) * scale           # [q_len, n]
+                s = np.where(seen, s, -np.inf)
+                m = np.where(any_seen, s.max(axis=1), 0.0)[:, None]
+                p = np.where(seen, np.exp(s - m), 0.0)
+                l = p.sum(axis=1, keepdims=True)
+                with np.errstate(invalid="ignore", divide="ignore"):
+                    o = np.where(l > 0, (p @ V[:, h, :]) / np.where(l > 0, l, 1.0), 0.0)
+                    lse[q0:q1, hq] = np.where(any_seen, (m + np.log(np.where(l > 0, l, 1.0)))[:, 0],
+                                              -np.inf)
+                out[q0:q1, hq] = o
+    return out, lse
+
+
 def merge_attention_states(out1, lse1, out2, lse2):
     """src/dense/offload_kv_attn.py:24-39 in fp32: lse = logaddexp(lse1, lse2),
     out = out1 * exp(lse1 - lse) + out2 * exp(lse2 - lse)."""

@@ -215,3 +215,63 @@ def test_entry_points_validate_before_touching_the_gpu(lib):
                                         None, None, None) == 0
     assert lib.kvc_copy_page_indices(None, 0, 1, None, None, 0, 1, None, None) == 0
     assert lib.kvc_merge_attention_states(None, None, None, None, 0, 128, None, None, None) == 0
+
+
+def _prefill_plan(lib, q_lens, kv_lens, hq=32, hkv=8, causal=1, cap=None):
+    qo = np.zeros(len(q_lens) + 1, np.int32)
+    np.cumsum(q_lens, out=qo[1:])
+    pages = [(k + 15) // 16 for k in kv_lens]
+    kvi = np.zeros(len(kv_lens) + 1, np.int32)
+    np.cumsum(pages, out=kvi[1:])
+    lpl = np.array([(k % 16 or 16) if k else 0 for k in kv_lens], np.int32)
+    sched = _lib.KvcPrefillSchedule()
+    img = np.zeros(cap if cap is not None else 8 * 4096, np.int32)
+    st = lib.kvc_prefill_plan(qo.ctypes.data, kvi.ctypes.data, lpl.ctypes.data, len(q_lens),
+                              hq, hkv, 128, 16, causal, ctypes.byref(sched), img.ctypes.data,
+                              img.size)
+    return st, sched, img[:max(sched.plan_ints, 0)].reshape(-1, 8), qo, kvi
+
+
+def test_prefill_plan_tiles_every_query_once_longest_first(lib):
+    q_lens, kv_lens = [1, 17, 40, 64, 130, 0, 33], [1, 40, 40, 300, 130, 12, 1000]
+    st, sched, rec, qo, kvi = _prefill_plan(lib, q_lens, kv_lens)
+    assert st == 0, lib.kvc_last_error()
+    assert sched.tile_tokens == 32 and sched.total_q == sum(q_lens)
+    assert (np.diff(rec[:, 6]) <= 0).all()                        # longest first
+    for b, (ql, kl) in enumerate(zip(q_lens, kv_lens)):
+        mine = rec[rec[:, 0] == b]
+        assert sorted(mine[:, 1].tolist()) == list(range(0, ql, 32))
+        for r in mine:
+            assert (r[2], r[3], r[4], r[5], r[7]) == (ql, kl, qo[b], kvi[b], kvi[b + 1] - kvi[b])
+            last = min(r[1] + 32, ql) - 1
+            keys = max(0, min(last + kl - ql + 1, kl))
+            assert r[6] == (keys + 63) // 64
+    assert sched.max_key_tiles == rec[:, 6].max()
+    # non-causal: every tile visits the whole cache
+    st, sched, rec, _, _ = _prefill_plan(lib, q_lens, kv_lens, causal=0)
+    assert st == 0
+    assert all(r[6] == (r[3] + 63) // 64 for r in rec)
+    # group 8 packs 16 tokens x 8 heads per tile
+    st, sched, rec, _, _ = _prefill_plan(lib, [100], [100], hq=16, hkv=2)
+    assert st == 0 and sched.tile_tokens == 16 and sched.num_items == 7
+
+
+def test_prefill_plan_reports_capacity_and_rejects_bad_input(lib):
+    st, sched, _, _, _ = _prefill_plan(lib, [100, 40], [100, 40], cap=8)
+    assert st == 4 and sched.plan_ints == 8 * (4 + 2)
+    assert b"plan buffer too small" in lib.kvc_last_error()
+    st, *_ = _prefill_plan(lib, [10], [10], hq=24, hkv=8)
+    assert st == 2                                                 # group 3
+    qo = np.array([0, 5, 3], np.int32)
+    kvi = np.array([0, 1, 2], np.int32)
+    lpl = np.array([5, 3], np.int32)
+    sched = _lib.KvcPrefillSchedule()
+    img = np.zeros(64, np.int32)
+    assert lib.kvc_prefill_plan(qo.ctypes.data, kvi.ctypes.data, lpl.ctypes.data, 2, 32, 8, 128,
+                                16, 1, ctypes.byref(sched), img.ctypes.data, 64) == 1
+    assert b"non-decreasing" in lib.kvc_last_error()
+    # zero items: the run is a no-op even with null pointers
+    st, sched, _, _, _ = _prefill_plan(lib, [0], [16])
+    assert st == 0 and sched.num_items == 0
+    assert lib.kvc_batch_prefill_run(ctypes.byref(sched), None, None, 4096, None, None, 16384,
+                                     1024, 1, None, 0, 0.1, None, 4096, None, None) == 0

@@ -1,0 +1,135 @@
+"""GPU parity of paged-KV prefill attention (continuation prefill, MFMA)
+against the fp32 CPU oracle: max-abs-error <= 2e-2 and mean-abs-error <= 2e-3
+on the bf16 output; lse within 2e-3."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_offloading_amd import workloads
+from gpu_offloading_amd.decode import BatchDecodeWithPagedKVCacheWrapper
+from gpu_offloading_amd.prefill import BatchPrefillWithPagedKVCacheWrapper
+from helpers import assert_attn_close, randn_bf16, u16
+from oracle import kv_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+WS = 16 * 1024 * 1024
+
+
+def _case(q_lens, kv_lens, hq, hkv, seed, d=128, extra_pages=8, device=None):
+    need = sum((ln + 15) // 16 for ln in kv_lens)
+    total = need + extra_pages
+    pool = orc.FifoPagePool(total, len(kv_lens), max(1, max((ln + 15) // 16 for ln in kv_lens)),
+                            free_order=workloads.randperm(total, seed))
+    for s, ln in enumerate(kv_lens):
+        pool.ensure_pages(s, (ln + 15) // 16)
+    g = torch.Generator().manual_seed(seed)
+    kc = torch.randn(total, 16, hkv, d, generator=g).to(torch.bfloat16)
+    vc = torch.randn(total, 16, hkv, d, generator=g).to(torch.bfloat16)
+    qo = np.zeros(len(q_lens) + 1, np.int32)
+    np.cumsum(q_lens, out=qo[1:])
+    kvi, lpl = orc.plan_decode(kv_lens)
+    idx = orc.page_indices(pool.block_table, range(len(kv_lens)), kvi)
+    q = randn_bf16((int(qo[-1]), hq, d), seed + 1, std=1.5, device=device)
+    return q, kc, vc, qo, kvi, idx, lpl
+
+
+def _run(gpu, q, kc, vc, qo, kvi, idx, lpl, hq, hkv, causal=True, out=None):
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(WS, dtype=torch.uint8, device=gpu))
+    w.plan(torch.from_numpy(qo), torch.from_numpy(kvi), torch.from_numpy(idx).to(gpu),
+           torch.from_numpy(lpl), num_qo_heads=hq, num_kv_heads=hkv, head_dim_qk=q.shape[-1],
+           page_size=16, causal=causal, q_data_type=torch.bfloat16)
+    res = w.run(q, (kc.to(gpu), vc.to(gpu)), out=out, return_lse=True)
+    torch.cuda.synchronize()
+    return res, w
+
+
+def _check(gpu, q_lens, kv_lens, hq, hkv, seed, causal=True):
+    q, kc, vc, qo, kvi, idx, lpl = _case(q_lens, kv_lens, hq, hkv, seed, device=gpu)
+    (out, lse), w = _run(gpu, q, kc, vc, qo, kvi, idx, lpl, hq, hkv, causal)
+    ref, ref_lse = orc.paged_prefill(u16(q), u16(kc), u16(vc), qo, kvi, idx, lpl, causal=causal)
+    assert_attn_close(out.float().cpu().numpy(), ref)
+    got_lse = lse.cpu().numpy()
+    fin = np.isfinite(ref_lse)
+    assert np.array_equal(np.isneginf(got_lse), ~fin)
+    assert np.abs(got_lse[fin] - ref_lse[fin]).max() < 2e-3
+    return w
+
+
+def test_prefill_mixed_batch_gqa4(gpu):
+    """Chunks at the tail of longer caches, chunks equal to the cache, a
+    one-token chunk, partial last pages and query tiles that straddle both
+    the chunk end and the causal diagonal."""
+    w = _check(gpu, [1, 17, 40, 64, 130, 5, 33], [1, 40, 40, 300, 130, 133, 1000], 32, 8, 30)
+    assert w.schedule.tile_tokens == 32 and w.schedule.num_items == 1 + 1 + 2 + 2 + 5 + 1 + 2
+
+
+@pytest.mark.parametrize("group", [1, 2, 8])
+def test_prefill_group_sizes(gpu, group):
+    hkv = 4 if group < 8 else 2
+    _check(gpu, [70, 3, 200], [70, 90, 333], hkv * group, hkv, 31 + group)
+
+
+def test_prefill_non_causal(gpu):
+    _check(gpu, [50, 8], [50, 300], 32, 8, 33, causal=False)
+
+
+def test_prefill_edge_cases(gpu):
+    """Empty chunks, a request with no pages, and a chunk longer than its
+    cache (its first queries see no key: output 0, lse -inf)."""
+    _check(gpu, [0, 20, 6, 0, 9], [12, 5, 0, 17, 40], 32, 8, 34)
+
+
+def test_prefill_nan_past_the_end(gpu):
+    """Tokens of a page past kv_len hold NaN bits; they must not leak."""
+    q, kc, vc, qo, kvi, idx, lpl = _case([37], [37], 32, 8, 35, device=gpu)
+    last = int(idx[kvi[1] - 1])
+    kc[last, 37 % 16:] = float("nan")
+    vc[last, 37 % 16:] = float("nan")
+    (out, _), _ = _run(gpu, q, kc, vc, qo, kvi, idx, lpl, 32, 8)
+    ref, _ = orc.paged_prefill(u16(q), u16(kc), u16(vc), qo, kvi, idx, lpl)
+    assert torch.isfinite(out).all()
+    assert_attn_close(out.float().cpu().numpy(), ref)
+
+
+def test_prefill_long_continuation(gpu):
+    """Two 384-token chunks after 640 and 0 cached tokens (many key tiles)."""
+    _check(gpu, [384, 384], [1024, 384], 32, 8, 36)
+
+
+def test_prefill_one_token_chunks_match_decode_kernel(gpu):
+    """A one-token chunk at the tail is a decode step: the MFMA prefill and the
+    decode kernel agree."""
+    kv_lens = [1, 16, 17, 500, 2000]
+    q, kc, vc, qo, kvi, idx, lpl = _case([1] * 5, kv_lens, 32, 8, 37, device=gpu)
+    (out, lse), _ = _run(gpu, q, kc, vc, qo, kvi, idx, lpl, 32, 8)
+    wd = BatchDecodeWithPagedKVCacheWrapper(torch.empty(128 << 20, dtype=torch.uint8, device=gpu))
+    wd.plan(torch.from_numpy(kvi), torch.from_numpy(idx).to(gpu), torch.from_numpy(lpl),
+            num_qo_heads=32, num_kv_heads=8, head_dim=128, page_size=16)
+    dout, dlse = wd.run(q, (kc.to(gpu), vc.to(gpu)), return_lse=True)
+    assert_attn_close(out.float().cpu().numpy(), dout.float().cpu().numpy())
+    assert (lse - dlse).abs().max().item() < 2e-3
+
+
+def test_prefill_strided_q_and_out(gpu):
+    q, kc, vc, qo, kvi, idx, lpl = _case([45, 20], [100, 20], 32, 8, 38, device=gpu)
+    big = torch.zeros(q.shape[0], 48, 128, dtype=torch.bfloat16, device=gpu)
+    big[:, 8:40] = q
+    qv = big[:, 8:40]
+    outbig = torch.full((q.shape[0], 40, 128), 7.0, dtype=torch.bfloat16, device=gpu)
+    (out, _), _ = _run(gpu, qv, kc, vc, qo, kvi, idx, lpl, 32, 8, out=outbig[:, 4:36])
+    ref, _ = orc.paged_prefill(u16(q), u16(kc), u16(vc), qo, kvi, idx, lpl)
+    assert_attn_close(out.float().cpu().numpy(), ref)
+    assert (outbig[:, :4] == 7).all() and (outbig[:, 36:] == 7).all()
+
+
+def test_prefill_rejects_unsupported(gpu):
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(WS, dtype=torch.uint8, device=gpu))
+    i = torch.tensor([0, 4], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="head_dim 128"):
+        w.plan(i, torch.tensor([0, 1], dtype=torch.int32), torch.zeros(1, dtype=torch.int32),
+               torch.tensor([4], dtype=torch.int32), 32, 8, 64, 16, causal=True)
+    with pytest.raises(RuntimeError, match="custom masks"):
+        w.plan(i, torch.tensor([0, 1], dtype=torch.int32), torch.zeros(1, dtype=torch.int32),
+               torch.tensor([4], dtype=torch.int32), 32, 8, 128, 16, causal=True,
+               custom_mask=torch.ones(4, dtype=torch.bool))

@@ -299,3 +299,89 @@ def test_planted_mistakes_are_caught():
     assert np.abs(bad_decode(headmap=lambda h: h % 2) - ref).max() > 1e-2  # interleaved map
     assert np.abs(bad_decode(scale=1.0) - ref).max() > 1e-2                # no 1/sqrt(d)
     assert np.abs(bad_decode(lpl_shift=-1) - ref).max() > 1e-3             # drops last token
+
+
+# ------------------------------------------------------------ paged prefill
+def _prefill_case(rng, q_lens, kv_lens, hq, hkv, d, nblocks=96):
+    pool = orc.FifoPagePool(nblocks, len(kv_lens), 64, free_order=rng.permutation(nblocks).tolist())
+    for s, ln in enumerate(kv_lens):
+        pool.ensure_pages(s, (ln + 15) // 16)
+    kc = rand_bf16(rng, (nblocks, 16, hkv, d))
+    vc = rand_bf16(rng, (nblocks, 16, hkv, d))
+    qo = np.zeros(len(q_lens) + 1, np.int32)
+    np.cumsum(q_lens, out=qo[1:])
+    q = rand_bf16(rng, (int(qo[-1]), hq, d), std=2.0)
+    kv_indptr, lpl = orc.plan_decode(kv_lens)
+    idx = orc.page_indices(pool.block_table, range(len(kv_lens)), kv_indptr)
+    return q, kc, vc, qo, kv_indptr, idx, lpl, pool.block_table
+
+
+def _sdpa_prefill(q_bits, kc, vc, qo, bt, kv_lens, mask_fn):
+    """torch SDPA per request, fp32, with a torch-built attention bias."""
+    q = torch.from_numpy(orc.bf16_to_f32(q_bits))
+    K = torch.from_numpy(orc.bf16_to_f32(kc))
+    V = torch.from_numpy(orc.bf16_to_f32(vc))
+    outs = []
+    for b, ln in enumerate(kv_lens):
+        qb = q[qo[b]:qo[b + 1]].transpose(0, 1).contiguous()          # [Hq, q_len, D]
+        pages = torch.from_numpy(bt[b, :(ln + 15) // 16].astype(np.int64))
+        Kb = K[pages].flatten(0, 1)[:ln].transpose(0, 1).contiguous()  # [Hkv, n, D]
+        Vb = V[pages].flatten(0, 1)[:ln].transpose(0, 1).contiguous()
+        o = torch.nn.functional.scaled_dot_product_attention(
+            qb[None], Kb[None], Vb[None], attn_mask=mask_fn(qb.shape[1], ln), enable_gqa=True)
+        outs.append(o[0].transpose(0, 1))
+    return torch.cat(outs).numpy()
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 64), (16, 2, 32)])
+def test_paged_prefill_matches_sdpa_lower_right_causal(hq, hkv, d):
+    """Chunks at the tail of the cache: torch's lower-right causal bias is
+    exactly 'query i sees keys j <= i + kv_len - q_len'."""
+    from torch.nn.attention.bias import causal_lower_right
+
+    rng = np.random.default_rng(21)
+    q_lens, kv_lens = [1, 17, 40, 64, 5], [1, 40, 40, 300, 133]
+    q, kc, vc, qo, kvi, idx, lpl, bt = _prefill_case(rng, q_lens, kv_lens, hq, hkv, d)
+    out, lse = orc.paged_prefill(q, kc, vc, qo, kvi, idx, lpl, causal=True)
+    ref = _sdpa_prefill(q, kc, vc, qo, bt, kv_lens, lambda m, n: causal_lower_right(m, n))
+    assert np.abs(out - ref).max() < 3e-5
+    # non-causal: no mask at all
+    out_nc, _ = orc.paged_prefill(q, kc, vc, qo, kvi, idx, lpl, causal=False)
+    ref_nc = _sdpa_prefill(q, kc, vc, qo, bt, kv_lens, lambda m, n: None)
+    assert np.abs(out_nc - ref_nc).max() < 3e-5
+    # a planted mistake -- the mask aligned to the start of the cache -- is caught
+    from torch.nn.attention.bias import causal_upper_left
+    wrong = _sdpa_prefill(q, kc, vc, qo, bt, kv_lens, lambda m, n: causal_upper_left(m, n))
+    assert np.abs(out - wrong).max() > 1e-2
+    # lse of the last row of request 3 (it sees every key) = logsumexp of its logits
+    b, row = 3, int(qo[4]) - 1
+    K = orc.bf16_to_f32(kc)[bt[b, :(kv_lens[b] + 15) // 16]].reshape(-1, hkv, d)[:kv_lens[b]]
+    qf = orc.bf16_to_f32(q)[row]
+    g = hq // hkv
+    logits = np.stack([qf[h] @ K[:, h // g].T for h in range(hq)]) / np.sqrt(d)
+    assert np.allclose(lse[row], torch.logsumexp(torch.from_numpy(logits), -1).numpy(), atol=1e-5)
+
+
+def test_paged_prefill_one_token_chunks_equal_decode():
+    """A one-token chunk at the tail is a decode step over the whole cache."""
+    rng = np.random.default_rng(22)
+    kv_lens = [1, 16, 17, 250]
+    q, kc, vc, qo, kvi, idx, lpl, bt = _prefill_case(rng, [1] * 4, kv_lens, 32, 8, 128)
+    out, lse = orc.paged_prefill(q, kc, vc, qo, kvi, idx, lpl, causal=True)
+    dec, dlse = orc.paged_decode(q, kc, vc, kvi, idx, lpl)
+    assert np.abs(out - dec).max() < 1e-5 and np.abs(lse - dlse).max() < 1e-5
+
+
+def test_paged_prefill_edge_cases():
+    rng = np.random.default_rng(23)
+    q, kc, vc, qo, kvi, idx, lpl, bt = _prefill_case(rng, [3, 0, 4], [2, 5, 4], 4, 2, 16)
+    out, lse = orc.paged_prefill(q, kc, vc, qo, kvi, idx, lpl, causal=True)
+    # request 0: 3 queries over 2 keys -- query 0 sees nothing (0, -inf),
+    # query 1 sees key 0 only (= V[0] of its kv head), query 2 sees both
+    V = orc.bf16_to_f32(vc)[bt[0, 0], :2]                      # [2, Hkv, D]
+    assert (out[0] == 0).all() and np.isneginf(lse[0]).all()
+    assert np.array_equal(out[1], V[0][[0, 0, 1, 1]])
+    assert np.isfinite(lse[2]).all()
+    # request 2: q_len == kv_len -- plain causal, query 0 sees key 0 only
+    V2 = orc.bf16_to_f32(vc)[bt[2, 0], :4]
+    assert np.array_equal(out[3], V2[0][[0, 0, 1, 1]])
