@@ -19,8 +19,9 @@ against it.  ``roofline`` is the decode-attention launch alone (streaming +
 merge kernel, bracketed by HIP events on the stream they run on) against the
 8 TB/s HBM3E peak.  ``extra`` carries the other rows of the metric: chunked-
 prefill append and gather GB/s (configuration 3), long-context decode GB/s
-(configuration 4) and swap host-link GB/s with decode slowdown
-(configuration 5).  ``cpu_baseline`` times the numpy oracle on one layer of
+(configuration 4), swap host-link GB/s with decode slowdown
+(configuration 5) and continuation-prefill TFLOP/s (the MFMA attention after
+the configuration 3 append).  ``cpu_baseline`` times the numpy oracle on one layer of
 the same workload on the host cores.
 
 Other modes used by the profiles (one kernel family each, few launches):
@@ -28,6 +29,8 @@ Other modes used by the profiles (one kernel family each, few launches):
   --mode decode2  configuration 2 decode, one layer, 10 launches
   --mode decode4  configuration 4 decode only (32 launches)
   --mode append3  configuration 3 append + gather, one layer, 10 launches each
+  --mode prefill3 continuation prefill after the cfg3 append (8 x 2048-token
+                  chunks over 2048 and 4096 cached tokens), 10 launches each
 """
 from __future__ import annotations
 
@@ -42,6 +45,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (no sparsity)
 # rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the configuration-2 decode launch
 # (calibrated HBM bytes per launch), written from `--mode decode2` runs.
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_lds_kernel_cfg2_mixtral_decode.md")
@@ -73,7 +77,7 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip configurations 3-5")
     p.add_argument("--mode", default="step",
-                   choices=["step", "copy", "decode2", "decode4", "append3"])
+                   choices=["step", "copy", "decode2", "decode4", "append3", "prefill3"])
     return p.parse_args()
 
 
@@ -310,6 +314,66 @@ def build_paged(torch, lens, hkv, d, seed, q_std=1.0, hq=32):
     return kc, vc, q, w
 
 
+def prefill_flops(q_lens, kv_lens, hq, d, causal=True):
+    """Algorithmic FLOPs of prefill attention: 4*D per (query row, head,
+    visible key) -- q.k and p.v, multiply + add."""
+    total = 0
+    for ql, kl in zip(q_lens, kv_lens):
+        if causal:
+            # query i sees min(kl, i + kl - ql + 1) keys (at least 0)
+            vis = sum(max(0, min(kl, i + kl - ql + 1)) for i in range(ql))
+        else:
+            vis = ql * kl
+        total += vis * hq * d * 4
+    return total
+
+
+def run_prefill(torch, seed, reps=10):
+    """Paged-KV continuation prefill (the attention after the cfg3 append):
+    8 requests x 2048-token chunks, Hq=32 / Hkv=8 / D=128, causal, over
+    (a) the chunk alone (first chunk) and (b) a 2048-token cached prefix plus
+    the chunk (second chunk).  Pages come from a seeded permuted pool."""
+    import numpy as np
+
+    from gpu_offloading_amd.prefill import BatchPrefillWithPagedKVCacheWrapper
+
+    hq, hkv, d = 32, 8, 128
+    res = {}
+    for name, q_len, kv_len in (("first_chunk", 2048, 2048), ("second_chunk", 2048, 4096)):
+        q_lens, kv_lens = [q_len] * 8, [kv_len] * 8
+        kc, vc, _, w0 = build_paged(torch, kv_lens, hkv, d, seed + 11, hq=hq)
+        qo = np.arange(0, 9 * q_len, q_len, dtype=np.int32)
+        kvi = np.arange(0, 9 * (kv_len // 16), kv_len // 16, dtype=np.int32)
+        lpl = np.full(8, 16, np.int32)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed + 12)
+        q = torch.randn(8 * q_len, hq, d, device="cuda", generator=g).to(torch.bfloat16)
+        w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1 << 20, dtype=torch.uint8, device="cuda"))
+        w.plan(torch.from_numpy(qo), torch.from_numpy(kvi), w0._indices, torch.from_numpy(lpl),
+               num_qo_heads=hq, num_kv_heads=hkv, head_dim_qk=d, page_size=16, causal=True,
+               q_data_type=torch.bfloat16)
+        out = torch.empty_like(q)
+        w.run(q, (kc, vc), out=out)
+        torch.cuda.synchronize()
+        e0, e1 = _events(torch)
+        e0.record()
+        for _ in range(reps):
+            w.run(q, (kc, vc), out=out)
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        f = prefill_flops(q_lens, kv_lens, hq, d)
+        assert torch.isfinite(out).all().item(), "non-finite prefill output"
+        res[name] = {"q_len": q_len, "kv_len": kv_len, "requests": 8, "us": t * 1e6,
+                     "TFLOPs": f / t / 1e12, "frac_of_peak": f / t / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                     "algorithmic_flops": f}
+        log(f"prefill {name}: 8 x {q_len} queries over {kv_len} keys, {t * 1e6:.1f} us, "
+            f"{f / t / 1e12:.1f} TFLOP/s ({f / t / 1e12 / MFMA_BF16_PEAK_TFLOPS:.1%} of bf16 MFMA peak)")
+        del kc, vc, q, w0, w, out
+        torch.cuda.empty_cache()
+    return res
+
+
 def run_cfg4(torch, seed, reps=32):
     from gpu_offloading_amd import workloads
 
@@ -525,6 +589,9 @@ def main():
     if args.mode == "decode4":
         run_cfg4(torch, args.seed)
         return
+    if args.mode == "prefill3":
+        print(json.dumps({"mode": "prefill3", **run_prefill(torch, args.seed)}), flush=True)
+        return
     if args.mode == "append3":
         print(json.dumps({"mode": "append3", **run_cfg3(torch, args.seed, layers=1)}), flush=True)
         return
@@ -535,6 +602,7 @@ def main():
         extra["cfg3_chunked_prefill"] = run_cfg3(torch, args.seed)
         extra["cfg4_long_context"] = run_cfg4(torch, args.seed)
         extra["cfg5_swap"] = run_cfg5(torch, args.seed)
+        extra["f2_continuation_prefill"] = run_prefill(torch, args.seed)
     cpu = None if args.no_cpu else run_cpu_baseline(args.seed)
     line = {
         "metric": "paged decode-attn HBM GB/s (% peak) + KV append/gather/swap GB/s, 1 GPU",
