@@ -5,9 +5,10 @@
 (:488-500), the block table (:504-519), ``seq_lens`` with its host mirror
 (:535-539), the dynamic page pool and its API (:578-582, 4185-4297),
 ``kv_snapshot`` / ``kv_restore`` / ``fill_kv_random`` (:4152-4183), the slot
-mapping and decode planning of a step (:1896-1955, 3475-3556) and the two
-kernels called per layer: the KV append (:2343-2347) and decode attention
-(:3907-3909).  It also adds the swap API the engine lacks (block eviction to
+mapping and decode planning of a step (:1896-1955, 3475-3556), the
+continuation-prefill planning (:1678-1751, 3649-3727) and the kernels called
+per layer: the KV append (:2343-2347), decode attention (:3907-3909) and
+paged prefill attention (:3939-3941).  It also adds the swap API the engine lacks (block eviction to
 pinned host memory and restore, on a side stream).
 
 All arithmetic runs in libkvc.so; this module only does host bookkeeping,
@@ -25,6 +26,7 @@ import torch
 from . import ops
 from .allocator import PagePool, pages_needed
 from .decode import BatchDecodeWithPagedKVCacheWrapper
+from .prefill import BatchPrefillWithPagedKVCacheWrapper
 
 __all__ = ["PagedKVCache", "SwapHandle"]
 
@@ -142,6 +144,10 @@ class PagedKVCache:
             num_segments=self._segments)
         self._plan_indices_gpu = torch.zeros(self.max_seqs * self.max_pages_per_seq,
                                              dtype=torch.int32, device=self.device)
+        self._prefill_wrapper = BatchPrefillWithPagedKVCacheWrapper(self._workspace_buf,
+                                                                    kv_layout="NHD")
+        self._prefill_indices_gpu = torch.zeros(self.max_seqs * self.max_pages_per_seq,
+                                                dtype=torch.int32, device=self.device)
 
     def _to_device(self, arr) -> torch.Tensor:
         """Async H2D of a small host array through a fresh pinned buffer."""
@@ -321,6 +327,58 @@ class PagedKVCache:
             torch.from_numpy(indptr), self._plan_indices_gpu[:total], torch.from_numpy(lpl),
             num_qo_heads=self.num_heads, num_kv_heads=self.num_kv_heads, head_dim=self.head_dim,
             page_size=self.page_size, pos_encoding_mode="NONE", q_data_type=self.dtype)
+
+    def plan_prefill(self, seq_ids: Sequence[int], chunk_lens: Sequence[int]) -> None:
+        """moe_engine.py:3649-3727: plan paged-KV prefill for continuation
+        chunks whose K/V are already appended and counted in ``seq_lens``
+        (query rows are the last ``chunk_lens[i]`` tokens of each sequence,
+        causal against everything cached)."""
+        self._require_gpu()
+        b = len(seq_ids)
+        if len(chunk_lens) != b:
+            raise ValueError("one chunk length per sequence")
+        self._sync_seqs(seq_ids)
+        ids = np.asarray(seq_ids, dtype=np.int64)
+        lens = self._seq_lens_cpu.numpy()[ids].astype(np.int64)
+        clen = np.asarray(chunk_lens, dtype=np.int64)
+        if (clen < 0).any() or (clen > lens).any():
+            raise ValueError("a chunk must be part of its sequence's cached tokens")
+        nblk = (lens + self.page_size - 1) // self.page_size
+        kv_indptr = np.zeros(b + 1, dtype=np.int32)
+        np.cumsum(nblk, out=kv_indptr[1:])
+        qo_indptr = np.zeros(b + 1, dtype=np.int32)
+        np.cumsum(clen, out=qo_indptr[1:])
+        lpl = lens % self.page_size
+        lpl = np.where((lpl == 0) & (lens != 0), self.page_size, lpl).astype(np.int32)
+        ops.copy_page_indices(self.block_table, self._to_device(kv_indptr),
+                              self._prefill_indices_gpu, seq_ids=self._to_device(ids.astype(np.int32)))
+        total = int(kv_indptr[b])
+        self._prefill_wrapper.plan(
+            torch.from_numpy(qo_indptr), torch.from_numpy(kv_indptr),
+            self._prefill_indices_gpu[:total], torch.from_numpy(lpl),
+            num_qo_heads=self.num_heads, num_kv_heads=self.num_kv_heads,
+            head_dim_qk=self.head_dim, page_size=self.page_size, causal=True,
+            q_data_type=self.dtype)
+
+    def prepare_prefill_chunk(self, seq_ids: Sequence[int], chunk_lens: Sequence[int]) -> torch.Tensor:
+        """Setup of a continuation-prefill step (moe_engine.py:1678-1751):
+        slot mapping of the chunk's tokens from the current lengths, then
+        ``seq_lens += chunk``, then the prefill plan.  Pages must already
+        cover the chunk.  Returns the chunk's slot mapping for ``append``."""
+        self._require_gpu()
+        self._sync_seqs(seq_ids)
+        slots = self.slot_mapping(seq_ids, chunk_lens)
+        self.advance(seq_ids, list(chunk_lens))
+        self.plan_prefill(seq_ids, chunk_lens)
+        return slots
+
+    def prefill(self, layer: int, q: torch.Tensor, out: Optional[torch.Tensor] = None,
+                return_lse: bool = False):
+        """Causal attention of the planned chunks' queries ``[sum(chunk), Hq, D]``
+        over the paged cache of ``layer`` (moe_engine.py:3939-3941)."""
+        self._require_gpu()
+        return self._prefill_wrapper.run(q, (self.k_cache[layer], self.v_cache[layer]),
+                                         out=out, return_lse=return_lse)
 
     def prepare_decode_step(self, seq_ids: Sequence[int], graph_n: Optional[int] = None) -> torch.Tensor:
         """Setup of a pure-decode step in the engine's order

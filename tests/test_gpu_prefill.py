@@ -133,3 +133,37 @@ def test_prefill_rejects_unsupported(gpu):
         w.plan(i, torch.tensor([0, 1], dtype=torch.int32), torch.zeros(1, dtype=torch.int32),
                torch.tensor([4], dtype=torch.int32), 32, 8, 128, 16, causal=True,
                custom_mask=torch.ones(4, dtype=torch.bool))
+
+
+def test_cache_continuation_prefill_flow(gpu):
+    """The engine's continuation path through PagedKVCache: per chunk,
+    ensure_pages -> prepare_prefill_chunk (slots, seq_lens += chunk, plan) ->
+    append -> prefill, twice; each chunk attends causally over everything
+    cached so far (oracle on the cache's own pages)."""
+    from gpu_offloading_amd.kv_cache import PagedKVCache
+
+    cache = PagedKVCache(1, 8, 128, max_seqs=3, max_seq_len=800, num_qo_heads=32,
+                         kv_page_budget=120, free_page_order=workloads.randperm(120, 40),
+                         device=gpu, workspace_bytes=1 << 20, staging_bytes=1 << 20)
+    seqs = [0, 1, 2]
+    g = torch.Generator(device=gpu).manual_seed(41)
+    for chunk in ([300, 17, 64], [200, 40, 1]):
+        for s, c in zip(seqs, chunk):
+            cache.ensure_pages(s, (int(cache._seq_lens_cpu[s]) + c + 15) // 16)
+        slots = cache.prepare_prefill_chunk(seqs, chunk)
+        n = sum(chunk)
+        k = torch.randn(n, 8, 128, device=gpu, generator=g).to(torch.bfloat16)
+        v = torch.randn(n, 8, 128, device=gpu, generator=g).to(torch.bfloat16)
+        q = torch.randn(n, 32, 128, device=gpu, generator=g).to(torch.bfloat16)
+        cache.append(0, k, v, slots)
+        out, lse = cache.prefill(0, q, return_lse=True)
+        torch.cuda.synchronize()
+        lens = [int(cache._seq_lens_cpu[s]) for s in seqs]
+        kvi, lpl = orc.plan_decode(lens)
+        idx = orc.page_indices(cache.block_table.cpu().numpy(), seqs, kvi)
+        qo = np.zeros(4, np.int32)
+        np.cumsum(chunk, out=qo[1:])
+        ref, ref_lse = orc.paged_prefill(u16(q), u16(cache.k_cache[0]), u16(cache.v_cache[0]),
+                                         qo, kvi, idx, lpl, causal=True)
+        assert_attn_close(out.float().cpu().numpy(), ref)
+        assert np.abs(lse.cpu().numpy() - ref_lse).max() < 2e-3
