@@ -103,6 +103,16 @@ SIGNATURES = {
     "kvc_batch_prefill_run": (c_int, [
         POINTER(KvcPrefillSchedule), _I32P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64,
         _I32P, c_int64, c_float, _P, c_int64, _P, _P]),
+    "kvc_reshape_and_cache_xpacked": (c_int, [
+        _P, _P, _P, _P, _P, c_int64, c_int32, c_int32, c_int32, c_int32, c_int64, c_int64,
+        c_int64, c_int64, c_int64, _P, _P]),
+    "kvc_paged_attention_v1": (c_int, [
+        _P, _P, c_int64, _P, _P, c_int32, c_int32, c_int32, c_int32, c_float, _I32P, c_int64,
+        c_int32, _I32P, c_int32, c_int32, c_int64, c_int32, c_int64, c_int64, _P]),
+    "kvc_paged_attention_v2": (c_int, [
+        _P, _P, _P, _P, c_int32, _P, c_int64, _P, _P, c_int32, c_int32, c_int32, c_int32,
+        c_float, _I32P, c_int64, c_int32, _I32P, c_int32, c_int32, c_int64, c_int32, c_int64,
+        c_int64, _P]),
     "kvc_merge_attention_states": (c_int, [
         _P, _P, _P, _P, c_int64, c_int32, _P, _P, _P]),
     "kvc_gather_blocks": (c_int, [

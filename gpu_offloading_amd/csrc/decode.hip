@@ -105,17 +105,6 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp<kDppQuadSwap1>(v));
-  v = fmaxf(v, dpp<kDppQuadSwap2>(v));
-  v = fmaxf(v, dpp<kDppRowRor4>(v));
-  v = fmaxf(v, dpp<kDppRowRor8>(v));
-  return v;
-}
-
-__device__ __forceinline__ float readlane_f(float v, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
 
 // First slot and page count of segment s.  The plan cuts the flattened page
 // list into equal parts, so both follow from the segment index, and a

@@ -99,6 +99,19 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// Max over the 16 lanes of a DPP row; every lane of the row gets it.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<kDppQuadSwap1>(v));
+  v = fmaxf(v, dpp<kDppQuadSwap2>(v));
+  v = fmaxf(v, dpp<kDppRowRor4>(v));
+  v = fmaxf(v, dpp<kDppRowRor8>(v));
+  return v;
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
 __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);
 }

@@ -1,0 +1,474 @@
+// vLLM's "x-packed" paged KV layout, the second on-device KV format of the
+// reference (its dense sandbox, src/dense/include/paged_transformer.py:85-92):
+//   key_cache   [num_blocks, H, D/x, block_size, x]   x = 16 bytes / element
+//   value_cache [num_blocks, H, D, block_size]
+// with vLLM's reshape_and_cache writing it (:290-294) and
+// paged_attention_v1/v2 reading it (:325-332; src/dense/scratch_examples/
+// vllm_paged_attn.py:274-288).  fp16 and bf16 (2-byte elements, x = 8),
+// head_size 128, block_size 16.
+//
+// In this layout one (block, head) is a contiguous 4 KB of K and 4 KB of V,
+// so decode streams straight into registers, no LDS staging:
+//   q.k : lane (token t = l%16, chunk group cg = l/16) loads the 16-byte
+//         chunks 4cg..4cg+3 of token t (dims 32cg..32cg+31), 16 dot2 per query
+//         head, then two xor-shuffles sum the 4 chunk groups;
+//   p.v : lane l loads dims 2l and 2l+1 over the page's 16 tokens (64 B);
+//         p is rounded to the cache dtype in (t, t+1) pairs -- as vLLM's kernel
+//         does before its value dot -- broadcast with v_readlane and folded
+//         with 8 dot2 per dim.
+// A workgroup (4 waves) owns one KV head x one 512-token partition (v2) or the
+// whole sequence (v1); wave w takes pages w, w+4, ...; the waves' softmax
+// states are merged through LDS.  v2 leaves vLLM's per-partition max logit,
+// exp-sum and normalised partial output, and a reduce kernel combines them.
+#include "kvc_common.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace kvc {
+namespace {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kBlock = 16;    // tokens per block
+constexpr int kD = 128;       // head size
+constexpr int kX = 8;         // elements per 16-byte chunk
+constexpr int kPart = 512;    // tokens per v2 partition (vLLM's)
+constexpr float kLn2 = 0.69314718055994530942f;
+constexpr float kLog2e = 1.44269504088896340736f;
+
+template <bool kBf16>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (kBf16)
+    return dot2_bf16(a, b, c);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a),
+                                  __builtin_bit_cast(half2_t, b), c, false);
+}
+
+// float -> element bits, round to nearest even.
+template <bool kBf16>
+__device__ __forceinline__ uint32_t to_elem(float f) {
+  if constexpr (kBf16)
+    return f32_to_bf16(f);
+  else
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+template <bool kBf16>
+__device__ __forceinline__ float from_elem(uint32_t bits) {
+  if constexpr (kBf16)
+    return __uint_as_float(bits << 16);
+  else
+    return static_cast<float>(__builtin_bit_cast(_Float16, uint16_t(bits)));
+}
+
+// ------------------------------------------------------------------ append
+struct XAppendArgs {
+  const uint16_t* key;
+  const uint16_t* value;
+  uint16_t* key_cache;
+  uint16_t* value_cache;
+  const int64_t* slots;
+  int64_t key_stride;      // elements between source tokens
+  int64_t value_stride;
+  int64_t block_stride;    // elements between cache blocks (K and V)
+  int64_t head_stride;     // elements between heads of a block (K and V)
+  int64_t num_slots;
+  int32_t num_heads;
+  int32_t* oob_count;
+};
+
+// One workgroup per token; thread j copies 16-byte chunk j of the token's
+// K row (chunk c of head h lands on key_cache[blk][h][c][off][0..7], the
+// same 8 elements) and scatters 8 elements of its V row to
+// value_cache[blk][h][d][off].
+__global__ __launch_bounds__(kThreads) void xpacked_append_kernel(XAppendArgs a) {
+  const int64_t i = blockIdx.x;
+  const int64_t slot = a.slots[i];
+  if (slot < 0) return;
+  if (slot >= a.num_slots) {
+    if (a.oob_count && threadIdx.x == 0) atomicAdd(a.oob_count, 1);
+    return;
+  }
+  const int64_t blk = slot / kBlock;
+  const int off = int(slot % kBlock);
+  const int chunks = a.num_heads * (kD / kX);
+  for (int j = threadIdx.x; j < chunks; j += kThreads) {
+    const int h = j / (kD / kX), c = j % (kD / kX);
+    const uint4 kv = *reinterpret_cast<const uint4*>(a.key + i * a.key_stride + int64_t(j) * kX);
+    const uint4 vv = *reinterpret_cast<const uint4*>(a.value + i * a.value_stride + int64_t(j) * kX);
+    const int64_t base = blk * a.block_stride + int64_t(h) * a.head_stride;
+    *reinterpret_cast<uint4*>(a.key_cache + base + (int64_t(c) * kBlock + off) * kX) = kv;
+    uint16_t* vdst = a.value_cache + base + int64_t(c) * kX * kBlock + off;
+    const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+    for (int e = 0; e < kX; ++e)
+      vdst[e * kBlock] = uint16_t(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xffffu);
+  }
+}
+
+// ------------------------------------------------------------------ decode
+struct XDecodeArgs {
+  const uint16_t* q;
+  int64_t q_stride;        // elements between sequences
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  int64_t block_stride;
+  int64_t head_stride;
+  int64_t num_blocks;
+  const int32_t* block_tables;
+  int64_t bt_stride;
+  int32_t bt_cols;         // entries per block-table row
+  const int32_t* seq_lens;
+  int32_t num_kv_heads;
+  int32_t max_parts;       // partitions per (sequence, head) in the v2 scratch
+  int32_t grid_parts;      // partitions launched (ceil(max_seq_len / 512))
+  float scale_log2;
+  uint16_t* out;           // [seqs][H][D]
+  float* exp_sums;         // [seqs][H][max_parts]
+  float* max_logits;
+  uint16_t* tmp_out;       // [seqs][H][max_parts][D]
+};
+
+template <int G, bool kBf16, bool kV1>
+__global__ __launch_bounds__(kThreads) void xpacked_decode_kernel(XDecodeArgs a) {
+  const int part = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int seq_len = max(a.seq_lens[b], 0);
+  const int t_begin = kV1 ? 0 : part * kPart;
+  const int t_end = kV1 ? seq_len : min(seq_len, t_begin + kPart);
+  if (!kV1 && t_begin >= seq_len) return;  // the reduce never reads it
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = lane & 15, cg = lane >> 4;
+  const int Hq = a.num_kv_heads * G;
+
+  uint32_t qw[G][16];  // dims 32cg .. 32cg+31 of each query head, as pairs
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const uint16_t* qp = a.q + int64_t(b) * a.q_stride + int64_t(h * G + g) * kD + 32 * cg;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 v = reinterpret_cast<const uint4*>(qp)[i];
+      qw[g][4 * i] = v.x; qw[g][4 * i + 1] = v.y; qw[g][4 * i + 2] = v.z; qw[g][4 * i + 3] = v.w;
+    }
+  }
+  float m[G], l[G], acc[G][2];
+#pragma unroll
+  for (int g = 0; g < G; ++g) { m[g] = kNegBig; l[g] = 0.f; acc[g][0] = acc[g][1] = 0.f; }
+
+  const int p_begin = t_begin / kBlock, p_end = (t_end + kBlock - 1) / kBlock;
+  const int32_t* bt = a.block_tables + int64_t(b) * a.bt_stride;
+  struct Regs { uint4 k[4], v[4]; };
+  auto block_of = [&](int p) __attribute__((always_inline)) {
+    const int32_t id = p < a.bt_cols ? bt[p] : -1;
+    return (id >= 0 && id < a.num_blocks) ? id : -1;
+  };
+  auto load = [&](Regs& r, int32_t id) __attribute__((always_inline)) {
+    const int64_t base = int64_t(id < 0 ? 0 : id) * a.block_stride + int64_t(h) * a.head_stride;
+    const uint16_t* kb = a.k_cache + base + (int64_t(4 * cg) * kBlock + t) * kX;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.k[i] = load_stream(kb + i * kBlock * kX);
+    const uint16_t* vb = a.v_cache + base + lane * 2 * kBlock;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r.v[j] = load_stream(vb + j * kX);
+  };
+  auto consume = [&](Regs& r, int p, int32_t id) __attribute__((always_inline)) {
+    const int valid = id < 0 ? 0 : min(kBlock, t_end - p * kBlock);
+    if (valid < kBlock) {
+      // tokens past the end: zero their V halves (they may hold NaN bits)
+      uint32_t* vw = reinterpret_cast<uint32_t*>(r.v);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int tok = 2 * (k & 7);
+        const uint32_t keep = (tok < valid ? 0xffffu : 0u) | (tok + 1 < valid ? 0xffff0000u : 0u);
+        vw[k] &= keep;
+      }
+    }
+    const bool live = t < valid;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        d = dot2<kBf16>(qw[g][4 * i + 0], r.k[i].x, d);
+        d = dot2<kBf16>(qw[g][4 * i + 1], r.k[i].y, d);
+        d = dot2<kBf16>(qw[g][4 * i + 2], r.k[i].z, d);
+        d = dot2<kBf16>(qw[g][4 * i + 3], r.k[i].w, d);
+      }
+      d += __shfl_xor(d, 16);
+      d += __shfl_xor(d, 32);
+      const float s = live ? d * a.scale_log2 : kNegBig;
+      const float m_new = fmaxf(m[g], row16_max(s));
+      const float pr = live ? fast_exp2(s - m_new) : 0.f;
+      const float alpha = fast_exp2(m[g] - m_new);
+      l[g] = fmaf(l[g], alpha, row16_sum(pr));
+      m[g] = m_new;
+      // (p[t], p[t+1]) as one element pair in even lanes, broadcast
+      const float nxt = __shfl_down(pr, 1, 16);
+      const uint32_t pair = to_elem<kBf16>(pr) | (to_elem<kBf16>(nxt) << 16);
+      uint32_t pw[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) pw[k] = __builtin_amdgcn_readlane(pair, 2 * k);
+      const uint32_t* vw = reinterpret_cast<const uint32_t*>(r.v);
+#pragma unroll
+      for (int dd = 0; dd < 2; ++dd) {
+        float o = acc[g][dd] * alpha;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o = dot2<kBf16>(pw[k], vw[8 * dd + k], o);
+        acc[g][dd] = o;
+      }
+    }
+  };
+
+  // Two register stages: page p + 4 is in flight while page p is consumed.
+  Regs ra, rb;
+  int p = p_begin + wave;
+  int32_t ida = p < p_end ? block_of(p) : -1;
+  if (p < p_end) load(ra, ida);
+  for (; p < p_end; p += 2 * kWaves) {
+    const int pb = p + kWaves;
+    int32_t idb = -1;
+    if (pb < p_end) { idb = block_of(pb); load(rb, idb); }
+    consume(ra, p, ida);
+    if (pb >= p_end) break;
+    const int pa = pb + kWaves;
+    if (pa < p_end) { ida = block_of(pa); load(ra, ida); }
+    consume(rb, pb, idb);
+  }
+
+  // Merge the 4 waves' states (lane l holds dims 2l, 2l+1 of every head).
+  __shared__ float s_m[kWaves][G], s_l[kWaves][G];
+  __shared__ float s_acc[kWaves][G][kD];
+  if (lane == 0)
+#pragma unroll
+    for (int g = 0; g < G; ++g) { s_m[wave][g] = m[g]; s_l[wave][g] = l[g]; }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    s_acc[wave][g][2 * lane] = acc[g][0];
+    s_acc[wave][g][2 * lane + 1] = acc[g][1];
+  }
+  __syncthreads();
+  // Thread j < G*D: head g = j / D, dim d = j % D.
+  for (int j = threadIdx.x; j < G * kD; j += kThreads) {
+    const int g = j / kD, d = j % kD;
+    float mx = kNegBig;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][g]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float sc = fast_exp2(s_m[w][g] - mx);
+      L = fmaf(s_l[w][g], sc, L);
+      O = fmaf(s_acc[w][g][d], sc, O);
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const int hq = h * G + g;
+    if constexpr (kV1) {
+      a.out[(int64_t(b) * Hq + hq) * kD + d] = uint16_t(to_elem<kBf16>(O * inv));
+    } else {
+      const int64_t row = (int64_t(b) * Hq + hq) * a.max_parts + part;
+      a.tmp_out[row * kD + d] = uint16_t(to_elem<kBf16>(O * inv));
+      if (d == 0) {
+        a.exp_sums[row] = L;
+        a.max_logits[row] = L > 0.f ? mx * kLn2 : -INFINITY;
+      }
+    }
+  }
+}
+
+// v2 reduce (vLLM's rule): M = max_p max_logits[p], w_p = exp_sums[p] *
+// exp(max_logits[p] - M), out = sum_p w_p tmp_out[p] / sum_p w_p.  One
+// partition: out = tmp_out[0].
+template <bool kBf16>
+__global__ __launch_bounds__(kD) void xpacked_reduce_kernel(XDecodeArgs a) {
+  const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int Hq = gridDim.x;
+  const int seq_len = max(a.seq_lens[b], 0);
+  const int parts = min((seq_len + kPart - 1) / kPart, a.grid_parts);
+  const int64_t row = (int64_t(b) * Hq + hq) * a.max_parts;
+  uint16_t* dst = a.out + (int64_t(b) * Hq + hq) * kD + d;
+  if (parts <= 1) {
+    *dst = parts == 1 ? a.tmp_out[row * kD + d] : uint16_t(0);
+    return;
+  }
+  float mx = -INFINITY;
+  for (int p = 0; p < parts; ++p) mx = fmaxf(mx, a.max_logits[row + p]);
+  float S = 0.f, O = 0.f;
+  for (int p = 0; p < parts; ++p) {
+    const float lg = a.max_logits[row + p];
+    const float w = lg == -INFINITY ? 0.f : a.exp_sums[row + p] * fast_exp2((lg - mx) * kLog2e);
+    S += w;
+    O = fmaf(w, from_elem<kBf16>(a.tmp_out[(row + p) * kD + d]), O);
+  }
+  *dst = uint16_t(to_elem<kBf16>(S > 0.f ? O / S : 0.f));
+}
+
+template <int G, bool kBf16>
+void launch_decode(const XDecodeArgs& a, bool v1, int parts, int hkv, int seqs, hipStream_t s) {
+  if (v1) {
+    xpacked_decode_kernel<G, kBf16, true><<<dim3(1, hkv, seqs), kThreads, 0, s>>>(a);
+  } else {
+    xpacked_decode_kernel<G, kBf16, false><<<dim3(parts, hkv, seqs), kThreads, 0, s>>>(a);
+    xpacked_reduce_kernel<kBf16><<<dim3(hkv * G, seqs), kD, 0, s>>>(a);
+  }
+}
+
+template <bool kBf16>
+bool dispatch(int group, const XDecodeArgs& a, bool v1, int parts, int hkv, int seqs,
+              hipStream_t s) {
+  switch (group) {
+    case 1: launch_decode<1, kBf16>(a, v1, parts, hkv, seqs, s); return true;
+    case 2: launch_decode<2, kBf16>(a, v1, parts, hkv, seqs, s); return true;
+    case 4: launch_decode<4, kBf16>(a, v1, parts, hkv, seqs, s); return true;
+    case 8: launch_decode<8, kBf16>(a, v1, parts, hkv, seqs, s); return true;
+    default: return false;
+  }
+}
+
+int paged_attention(bool v1, void* out, float* exp_sums, float* max_logits, void* tmp_out,
+                    int32_t max_num_partitions, const void* query, int64_t q_stride,
+                    const void* key_cache, const void* value_cache, int32_t num_seqs,
+                    int32_t num_heads, int32_t num_kv_heads, int32_t head_size, float scale,
+                    const int32_t* block_tables, int64_t block_table_stride,
+                    int32_t max_blocks_per_seq, const int32_t* seq_lens, int32_t block_size,
+                    int32_t max_seq_len, int64_t num_blocks, int32_t dtype,
+                    int64_t kv_block_stride, int64_t kv_head_stride, void* stream) {
+  KVC_REQUIRE(num_seqs >= 0 && max_seq_len >= 0, KVC_ERR_INVALID_ARG, "negative size");
+  if (num_seqs == 0) return ok();
+  KVC_REQUIRE(out && query && key_cache && value_cache && block_tables && seq_lens,
+              KVC_ERR_INVALID_ARG, "null pointer");
+  KVC_REQUIRE(head_size == kD && block_size == kBlock, KVC_ERR_UNSUPPORTED,
+              "x-packed attention supports head_size 128 and block_size 16");
+  KVC_REQUIRE(dtype == KVC_DTYPE_FP16 || dtype == KVC_DTYPE_BF16, KVC_ERR_UNSUPPORTED,
+              "dtype must be fp16 or bf16");
+  KVC_REQUIRE(num_kv_heads > 0 && num_heads % num_kv_heads == 0, KVC_ERR_INVALID_ARG,
+              "num_heads must be a multiple of num_kv_heads");
+  const int group = num_heads / num_kv_heads;
+  KVC_REQUIRE(num_blocks > 0 && max_blocks_per_seq >= 0 &&
+                  block_table_stride >= max_blocks_per_seq,
+              KVC_ERR_INVALID_ARG, "bad block table / num_blocks");
+  KVC_REQUIRE(kv_head_stride >= int64_t(kD) * kBlock &&
+                  kv_block_stride >= kv_head_stride * num_kv_heads,
+              KVC_ERR_INVALID_ARG, "cache strides smaller than a head / block");
+  KVC_REQUIRE(q_stride >= int64_t(num_heads) * kD, KVC_ERR_INVALID_ARG,
+              "query stride smaller than num_heads * head_size");
+  KVC_REQUIRE(aligned(query, 16) && aligned(key_cache, 16) && aligned(value_cache, 16) &&
+                  aligned(out, 2) && q_stride % 8 == 0 && kv_block_stride % 8 == 0 &&
+                  kv_head_stride % 8 == 0,
+              KVC_ERR_ALIGNMENT, "query/cache pointers and strides must be 16-byte aligned");
+  const int parts = (max_seq_len + kPart - 1) / kPart;
+  if (!v1) {
+    KVC_REQUIRE(exp_sums && max_logits && tmp_out, KVC_ERR_INVALID_ARG,
+                "v2 needs exp_sums, max_logits and tmp_out");
+    KVC_REQUIRE(max_num_partitions >= parts, KVC_ERR_WORKSPACE,
+                "v2 scratch holds " + std::to_string(max_num_partitions) +
+                    " partitions, max_seq_len needs " + std::to_string(parts));
+  }
+  XDecodeArgs a;
+  a.q = static_cast<const uint16_t*>(query);
+  a.q_stride = q_stride;
+  a.k_cache = static_cast<const uint16_t*>(key_cache);
+  a.v_cache = static_cast<const uint16_t*>(value_cache);
+  a.block_stride = kv_block_stride;
+  a.head_stride = kv_head_stride;
+  a.num_blocks = num_blocks;
+  a.block_tables = block_tables;
+  a.bt_stride = block_table_stride;
+  a.bt_cols = max_blocks_per_seq;
+  a.seq_lens = seq_lens;
+  a.num_kv_heads = num_kv_heads;
+  a.max_parts = v1 ? 1 : max_num_partitions;
+  a.grid_parts = parts;
+  a.scale_log2 = scale * kLog2e;
+  a.out = static_cast<uint16_t*>(out);
+  a.exp_sums = exp_sums;
+  a.max_logits = max_logits;
+  a.tmp_out = static_cast<uint16_t*>(tmp_out);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int grid_parts = std::max(parts, 1);
+  const bool okd = dtype == KVC_DTYPE_BF16
+                       ? dispatch<true>(group, a, v1, grid_parts, num_kv_heads, num_seqs, s)
+                       : dispatch<false>(group, a, v1, grid_parts, num_kv_heads, num_seqs, s);
+  KVC_REQUIRE(okd, KVC_ERR_UNSUPPORTED, "group (num_heads / num_kv_heads) must be 1, 2, 4 or 8");
+  KVC_LAUNCH_CHECK();
+  return ok();
+}
+
+}  // namespace
+}  // namespace kvc
+
+using namespace kvc;
+
+extern "C" int kvc_reshape_and_cache_xpacked(
+    const void* key, const void* value, void* key_cache, void* value_cache,
+    const int64_t* slot_mapping, int64_t num_tokens, int32_t num_heads, int32_t head_size,
+    int32_t block_size, int32_t x, int64_t num_blocks, int64_t key_token_stride,
+    int64_t value_token_stride, int64_t cache_block_stride, int64_t cache_head_stride,
+    int32_t* oob_count, void* stream) {
+  KVC_REQUIRE(num_tokens >= 0, KVC_ERR_INVALID_ARG, "num_tokens < 0");
+  if (num_tokens == 0) return ok();
+  KVC_REQUIRE(key && value && key_cache && value_cache && slot_mapping, KVC_ERR_INVALID_ARG,
+              "null pointer");
+  KVC_REQUIRE(head_size == kD && block_size == kBlock && x == kX, KVC_ERR_UNSUPPORTED,
+              "x-packed layout supports head_size 128, block_size 16 and x = 8 (2-byte types)");
+  KVC_REQUIRE(num_heads > 0 && num_blocks > 0, KVC_ERR_INVALID_ARG, "non-positive shape");
+  KVC_REQUIRE(num_tokens < (int64_t(1) << 31), KVC_ERR_INVALID_ARG, "too many tokens");
+  KVC_REQUIRE(key_token_stride >= int64_t(num_heads) * kD &&
+                  value_token_stride >= int64_t(num_heads) * kD,
+              KVC_ERR_INVALID_ARG, "source token stride smaller than a row");
+  KVC_REQUIRE(cache_head_stride >= int64_t(kD) * kBlock &&
+                  cache_block_stride >= cache_head_stride * num_heads,
+              KVC_ERR_INVALID_ARG, "cache strides smaller than a head / block");
+  KVC_REQUIRE(aligned(key, 16) && aligned(value, 16) && aligned(key_cache, 16) &&
+                  aligned(value_cache, 2) && key_token_stride % 8 == 0 &&
+                  value_token_stride % 8 == 0 && cache_block_stride % 8 == 0 &&
+                  cache_head_stride % 8 == 0,
+              KVC_ERR_ALIGNMENT, "key/value/cache pointers and strides must be 16-byte aligned");
+  XAppendArgs a;
+  a.key = static_cast<const uint16_t*>(key);
+  a.value = static_cast<const uint16_t*>(value);
+  a.key_cache = static_cast<uint16_t*>(key_cache);
+  a.value_cache = static_cast<uint16_t*>(value_cache);
+  a.slots = slot_mapping;
+  a.key_stride = key_token_stride;
+  a.value_stride = value_token_stride;
+  a.block_stride = cache_block_stride;
+  a.head_stride = cache_head_stride;
+  a.num_slots = num_blocks * kBlock;
+  a.num_heads = num_heads;
+  a.oob_count = oob_count;
+  xpacked_append_kernel<<<dim3(unsigned(num_tokens)), kThreads, 0,
+                          static_cast<hipStream_t>(stream)>>>(a);
+  KVC_LAUNCH_CHECK();
+  return ok();
+}
+
+extern "C" int kvc_paged_attention_v1(
+    void* out, const void* query, int64_t q_stride, const void* key_cache,
+    const void* value_cache, int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+    int32_t head_size, float scale, const int32_t* block_tables, int64_t block_table_stride,
+    int32_t max_blocks_per_seq, const int32_t* seq_lens, int32_t block_size,
+    int32_t max_seq_len, int64_t num_blocks, int32_t dtype, int64_t kv_block_stride,
+    int64_t kv_head_stride, void* stream) {
+  return paged_attention(true, out, nullptr, nullptr, nullptr, 1, query, q_stride, key_cache,
+                         value_cache, num_seqs, num_heads, num_kv_heads, head_size, scale,
+                         block_tables, block_table_stride, max_blocks_per_seq, seq_lens,
+                         block_size, max_seq_len, num_blocks, dtype, kv_block_stride,
+                         kv_head_stride, stream);
+}
+
+extern "C" int kvc_paged_attention_v2(
+    void* out, float* exp_sums, float* max_logits, void* tmp_out, int32_t max_num_partitions,
+    const void* query, int64_t q_stride, const void* key_cache, const void* value_cache,
+    int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads, int32_t head_size, float scale,
+    const int32_t* block_tables, int64_t block_table_stride, int32_t max_blocks_per_seq,
+    const int32_t* seq_lens, int32_t block_size, int32_t max_seq_len, int64_t num_blocks,
+    int32_t dtype, int64_t kv_block_stride, int64_t kv_head_stride, void* stream) {
+  return paged_attention(false, out, exp_sums, max_logits, tmp_out, max_num_partitions, query,
+                         q_stride, key_cache, value_cache, num_seqs, num_heads, num_kv_heads,
+                         head_size, scale, block_tables, block_table_stride, max_blocks_per_seq,
+                         seq_lens, block_size, max_seq_len, num_blocks, dtype, kv_block_stride,
+                         kv_head_stride, stream);
+}

@@ -33,6 +33,9 @@ __all__ = [
     "swap_out_blocks",
     "swap_in_blocks",
     "block_bytes",
+    "reshape_and_cache",
+    "paged_attention_v1",
+    "paged_attention_v2",
 ]
 
 
@@ -389,3 +392,153 @@ def swap_in_blocks(host: torch.Tensor, block_ids: torch.Tensor,
                   kc.data_ptr(), vc.data_ptr(), stride, bb, nb, staging.data_ptr(),
                   staging.numel() * staging.element_size(), _oob_ptr(oob_count),
                   _stream_handle(dev, stream))
+
+
+# --------------------------------------------------------------------------
+# (f3) vLLM's x-packed layout: reshape_and_cache + paged_attention_v1/v2
+# --------------------------------------------------------------------------
+_XDTYPES = {torch.float16: 0, torch.bfloat16: 1}
+
+
+def _check_xpacked(key_cache: torch.Tensor, value_cache: torch.Tensor):
+    """[nb, H, D/x, bs, x] and [nb, H, D, bs] with packed inner dimensions
+    and equal block / head strides; returns (nb, H, D, bs, x)."""
+    if key_cache.dim() != 5 or value_cache.dim() != 4:
+        _fail("x-packed caches must be key [nb, H, D/x, bs, x] and value [nb, H, D, bs]")
+    nb, h, dx, bs, x = key_cache.shape
+    d = dx * x
+    if tuple(value_cache.shape) != (nb, h, d, bs):
+        _fail(f"value_cache must be [{nb}, {h}, {d}, {bs}], got {tuple(value_cache.shape)}")
+    if key_cache.dtype not in _XDTYPES or value_cache.dtype != key_cache.dtype:
+        _fail("x-packed caches must be float16 or bfloat16, both the same")
+    if x != 16 // key_cache.element_size():
+        _fail(f"x must be 16 bytes / element = {16 // key_cache.element_size()}, got {x}")
+    if (key_cache.stride()[2:] != (bs * x, x, 1) or value_cache.stride()[2:] != (bs, 1)
+            or key_cache.stride()[:2] != value_cache.stride()[:2]):
+        _fail("x-packed caches: inner dimensions packed, block/head strides equal for K and V")
+    return nb, h, d, bs, x
+
+
+def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tensor,
+                      value_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                      kv_cache_dtype: str = "auto", k_scale: Optional[torch.Tensor] = None,
+                      v_scale: Optional[torch.Tensor] = None, *,
+                      oob_count: Optional[torch.Tensor] = None,
+                      stream: Optional[torch.cuda.Stream] = None) -> None:
+    """vLLM's ``reshape_and_cache`` into the x-packed layout, as the dense
+    sandbox calls it (src/dense/include/paged_transformer.py:290-294): key /
+    value ``[num_tokens, H, D]`` (token stride free, heads packed), key_cache
+    ``[nb, H, D/x, 16, x]``, value_cache ``[nb, H, D, 16]``; a negative slot is
+    padding.  Bit copies; ``kv_cache_dtype`` must be "auto"."""
+    if kv_cache_dtype != "auto":
+        _fail(f"kv_cache_dtype={kv_cache_dtype!r} is not supported (only 'auto')")
+    dev = _check_cuda(key, value, key_cache, value_cache, slot_mapping)
+    nb, h, d, bs, x = _check_xpacked(key_cache, value_cache)
+    if slot_mapping.dtype != torch.int64 or slot_mapping.dim() != 1 or not slot_mapping.is_contiguous():
+        _fail("slot_mapping must be a contiguous 1-D int64 tensor")
+    n = slot_mapping.numel()
+    for name, t in (("key", key), ("value", value)):
+        if t.dim() != 3 or tuple(t.shape[1:]) != (h, d) or t.shape[0] < n:
+            _fail(f"{name} must be [>= {n}, {h}, {d}], got {tuple(t.shape)}")
+        if t.stride(2) != 1 or t.stride(1) != d or t.dtype != key_cache.dtype:
+            _fail(f"{name}: heads must be packed and the dtype must match the cache")
+    _lib.call("kvc_reshape_and_cache_xpacked", key.data_ptr(), value.data_ptr(),
+              key_cache.data_ptr(), value_cache.data_ptr(), slot_mapping.data_ptr(), n, h, d,
+              bs, x, nb, key.stride(0), value.stride(0), key_cache.stride(0),
+              key_cache.stride(1), _oob_ptr(oob_count), _stream_handle(dev, stream))
+
+
+def _paged_attention(v2: bool, out, exp_sums, max_logits, tmp_out, query, key_cache,
+                     value_cache, num_kv_heads, scale, block_tables, seq_lens, block_size,
+                     max_seq_len, alibi_slopes, kv_cache_dtype, k_scale, v_scale, extra, stream):
+    if alibi_slopes is not None:
+        _fail("alibi_slopes are not supported")
+    if kv_cache_dtype != "auto":
+        _fail(f"kv_cache_dtype={kv_cache_dtype!r} is not supported (only 'auto')")
+    if any(int(v) != 0 for v in extra[:2]) or (len(extra) > 3 and int(extra[3]) != 0):
+        _fail("block-sparse attention is not supported")
+    for sc in (k_scale, v_scale):
+        if sc is not None and float(sc) != 1.0:
+            _fail("k/v scales other than 1.0 are not supported (no fp8 cache)")
+    dev = _check_cuda(out, query, key_cache, value_cache, block_tables, seq_lens,
+                      exp_sums, max_logits, tmp_out)
+    nb, hkv, d, bs, x = _check_xpacked(key_cache, value_cache)
+    if hkv != num_kv_heads:
+        _fail(f"num_kv_heads={num_kv_heads} but the cache holds {hkv} heads")
+    if block_size != bs:
+        _fail(f"block_size={block_size} but the cache blocks hold {bs} tokens")
+    if query.dim() != 3 or query.shape[2] != d or query.dtype != key_cache.dtype:
+        _fail(f"query must be [num_seqs, num_heads, {d}] of the cache dtype")
+    seqs, hq = query.shape[0], query.shape[1]
+    if query.stride(2) != 1 or query.stride(1) != d:
+        _fail("query: heads must be packed")
+    if tuple(out.shape) != (seqs, hq, d) or not out.is_contiguous() or out.dtype != query.dtype:
+        _fail(f"out must be a contiguous [{seqs}, {hq}, {d}] tensor of the query dtype")
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.stride(1) != 1:
+        _fail("block_tables must be int32 [num_seqs, max_blocks] with packed rows")
+    if block_tables.shape[0] < seqs or seq_lens.dtype != torch.int32 or seq_lens.numel() < seqs:
+        _fail("block_tables / seq_lens need one row / entry per sequence")
+    if not seq_lens.is_contiguous():
+        _fail("seq_lens must be contiguous")
+    dt = _XDTYPES[key_cache.dtype]
+    common = (query.data_ptr(), query.stride(0), key_cache.data_ptr(), value_cache.data_ptr(),
+              seqs, hq, num_kv_heads, d, float(scale), block_tables.data_ptr(),
+              block_tables.stride(0), block_tables.shape[1], seq_lens.data_ptr(), bs,
+              int(max_seq_len), nb, dt, key_cache.stride(0), key_cache.stride(1),
+              _stream_handle(dev, stream))
+    if not v2:
+        _lib.call("kvc_paged_attention_v1", out.data_ptr(), *common)
+        return
+    parts = exp_sums.shape[-1] if exp_sums.dim() == 3 else 0
+    for name, t, shp in (("exp_sums", exp_sums, (seqs, hq, parts)),
+                         ("max_logits", max_logits, (seqs, hq, parts)),
+                         ("tmp_out", tmp_out, (seqs, hq, parts, d))):
+        if tuple(t.shape) != shp or not t.is_contiguous():
+            _fail(f"{name} must be a contiguous {shp} tensor")
+    if exp_sums.dtype != torch.float32 or max_logits.dtype != torch.float32 \
+            or tmp_out.dtype != query.dtype:
+        _fail("exp_sums / max_logits are float32, tmp_out has the query dtype")
+    _lib.call("kvc_paged_attention_v2", out.data_ptr(), exp_sums.data_ptr(),
+              max_logits.data_ptr(), tmp_out.data_ptr(), parts, *common)
+
+
+def paged_attention_v1(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
+                       value_cache: torch.Tensor, num_kv_heads: int, scale: float,
+                       block_tables: torch.Tensor, seq_lens: torch.Tensor, block_size: int,
+                       max_seq_len: int, alibi_slopes: Optional[torch.Tensor] = None,
+                       kv_cache_dtype: str = "auto", k_scale=None, v_scale=None,
+                       tp_rank: int = 0, blocksparse_local_blocks: int = 0,
+                       blocksparse_vert_stride: int = 0, blocksparse_block_size: int = 64,
+                       blocksparse_head_sliding_step: int = 0, *,
+                       stream: Optional[torch.cuda.Stream] = None) -> None:
+    """vLLM's ``paged_attention_v1`` over the x-packed layout
+    (src/dense/scratch_examples/vllm_paged_attn.py:274-279): one pass per
+    (sequence, KV head) over the whole context, written to ``out``."""
+    _paged_attention(False, out, None, None, None, query, key_cache, value_cache, num_kv_heads,
+                     scale, block_tables, seq_lens, block_size, max_seq_len, alibi_slopes,
+                     kv_cache_dtype, k_scale, v_scale,
+                     (blocksparse_local_blocks, blocksparse_vert_stride, blocksparse_block_size,
+                      blocksparse_head_sliding_step), stream)
+
+
+def paged_attention_v2(out: torch.Tensor, exp_sums: torch.Tensor, max_logits: torch.Tensor,
+                       tmp_out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
+                       value_cache: torch.Tensor, num_kv_heads: int, scale: float,
+                       block_tables: torch.Tensor, seq_lens: torch.Tensor, block_size: int,
+                       max_seq_len: int, alibi_slopes: Optional[torch.Tensor] = None,
+                       kv_cache_dtype: str = "auto", k_scale=None, v_scale=None,
+                       tp_rank: int = 0, blocksparse_local_blocks: int = 0,
+                       blocksparse_vert_stride: int = 0, blocksparse_block_size: int = 64,
+                       blocksparse_head_sliding_step: int = 0, *,
+                       stream: Optional[torch.cuda.Stream] = None) -> None:
+    """vLLM's ``paged_attention_v2`` over the x-packed layout, as the dense
+    sandbox calls it (src/dense/include/paged_transformer.py:325-332): the
+    context is cut into 512-token partitions whose max logit, exp-sum and
+    normalised output land in ``max_logits`` / ``exp_sums`` / ``tmp_out``
+    ([num_seqs, num_heads, partitions(, D)], partitions >=
+    ceil(max_seq_len / 512)), then combined into ``out``."""
+    _paged_attention(True, out, exp_sums, max_logits, tmp_out, query, key_cache, value_cache,
+                     num_kv_heads, scale, block_tables, seq_lens, block_size, max_seq_len,
+                     alibi_slopes, kv_cache_dtype, k_scale, v_scale,
+                     (blocksparse_local_blocks, blocksparse_vert_stride, blocksparse_block_size,
+                      blocksparse_head_sliding_step), stream)

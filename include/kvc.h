@@ -222,6 +222,59 @@ int kvc_batch_prefill_run(
     float sm_scale, void* out, int64_t out_token_stride, float* lse, void* stream);
 
 /* ------------------------------------------------------------------------
+ * (f3) vLLM's x-packed paged layout (src/dense/include/paged_transformer.py:85-92):
+ *   key_cache   [num_blocks][H][head_size/x][block_size][x]   x = 16 B / element
+ *   value_cache [num_blocks][H][head_size][block_size]
+ * Strides are in elements; the innermost three (two) dimensions are packed,
+ * block and head strides are parameters (the same for K and V).
+ * Supported: 2-byte elements (x = 8), head_size 128, block_size 16.
+ *
+ * kvc_reshape_and_cache_xpacked replaces vLLM _C reshape_and_cache as called
+ * at paged_transformer.py:290-294: for every token i with slot s >= 0,
+ *   key_cache[s/16][h][d/8][s%16][d%8] = key[i][h][d]
+ *   value_cache[s/16][h][d][s%16]      = value[i][h][d]
+ * (bit copies; slot < 0 skipped; slot >= num_blocks*16 skipped and counted
+ * in the optional *oob_count).
+ * ---------------------------------------------------------------------- */
+enum { KVC_DTYPE_FP16 = 0, KVC_DTYPE_BF16 = 1 };
+
+int kvc_reshape_and_cache_xpacked(
+    const void* key, const void* value, void* key_cache, void* value_cache,
+    const int64_t* slot_mapping, int64_t num_tokens, int32_t num_heads, int32_t head_size,
+    int32_t block_size, int32_t x, int64_t num_blocks, int64_t key_token_stride,
+    int64_t value_token_stride, int64_t cache_block_stride, int64_t cache_head_stride,
+    int32_t* oob_count, void* stream);
+
+/* Decode attention over the x-packed layout; replaces vLLM _C
+ * paged_attention_v1 / paged_attention_v2 as called at
+ * paged_transformer.py:325-332 and scratch_examples/vllm_paged_attn.py:274-288:
+ *   out[b][hq] = softmax_t(scale q[b][hq].K[t][hq/group]) . V[t][hq/group]
+ * over the seq_lens[b] tokens of block_tables[b][...], group =
+ * num_heads / num_kv_heads (1/2/4/8), fp32 accumulation, p rounded to the
+ * cache dtype before the value product (as vLLM's kernel).  out is
+ * [num_seqs][num_heads][head_size] (packed).  v2 splits every sequence into
+ * 512-token partitions and leaves vLLM's scratch: max_logits[b][hq][p] (max
+ * scaled logit), exp_sums[b][hq][p] (sum of exp(logit - max)) and
+ * tmp_out[b][hq][p][:] (the partition's normalised output), each with
+ * max_num_partitions >= ceil(max_seq_len / 512) entries per (b, hq), then
+ * combines them.  max_seq_len must bound every seq_lens[b]. */
+int kvc_paged_attention_v1(
+    void* out, const void* query, int64_t q_stride, const void* key_cache,
+    const void* value_cache, int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+    int32_t head_size, float scale, const int32_t* block_tables, int64_t block_table_stride,
+    int32_t max_blocks_per_seq, const int32_t* seq_lens, int32_t block_size,
+    int32_t max_seq_len, int64_t num_blocks, int32_t dtype, int64_t kv_block_stride,
+    int64_t kv_head_stride, void* stream);
+
+int kvc_paged_attention_v2(
+    void* out, float* exp_sums, float* max_logits, void* tmp_out, int32_t max_num_partitions,
+    const void* query, int64_t q_stride, const void* key_cache, const void* value_cache,
+    int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads, int32_t head_size, float scale,
+    const int32_t* block_tables, int64_t block_table_stride, int32_t max_blocks_per_seq,
+    const int32_t* seq_lens, int32_t block_size, int32_t max_seq_len, int64_t num_blocks,
+    int32_t dtype, int64_t kv_block_stride, int64_t kv_head_stride, void* stream);
+
+/* ------------------------------------------------------------------------
  * (a8) Merge two attention states, fp32 math:
  *   lse = logaddexp(lse1, lse2); out = out1*e^(lse1-lse) + out2*e^(lse2-lse)
  * Restates src/dense/offload_kv_attn.py:24-39 on the device.  out* are bf16

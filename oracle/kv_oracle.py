@@ -298,6 +298,80 @@ def merge_attention_states(out1, lse1, out2, lse2):
     return o1 * w1 + o2 * w2, new[..., 0]
 
 
+# ------------------------------------------------- x-packed layout (f3)
+
+
+def elem_to_f32(x: np.ndarray, dtype: str) -> np.ndarray:
+    """2-byte element bits (uint16) to float32: "bf16" or "fp16"."""
+    if dtype == "bf16":
+        return bf16_to_f32(x)
+    return np.asarray(x, np.uint16).view(np.float16).astype(np.float32)
+
+
+def reshape_and_cache_xpacked(key: np.ndarray, value: np.ndarray, key_cache: np.ndarray,
+                              value_cache: np.ndarray, slot_mapping: np.ndarray) -> None:
+    """vLLM reshape_and_cache as called at src/dense/include/paged_transformer.py:290-294,
+    in place on bits: key_cache [nb, H, D/x, bs, x], value_cache [nb, H, D, bs];
+    token i with slot s >= 0 goes to block s // bs, offset s % bs."""
+    nb, H, Dx, bs, x = key_cache.shape
+    for i, s in enumerate(np.asarray(slot_mapping, np.int64)):
+        if s < 0 or s >= nb * bs:
+            continue
+        blk, off = divmod(int(s), bs)
+        key_cache[blk, :, :, off, :] = key[i].reshape(H, Dx, x)
+        value_cache[blk, :, :, off] = value[i]
+
+
+def xpacked_to_nhd(key_cache: np.ndarray, value_cache: np.ndarray):
+    """The x-packed caches re-laid as the flat NHD layout [nb, bs, H, D]."""
+    nb, H, Dx, bs, x = key_cache.shape
+    k = key_cache.transpose(0, 3, 1, 2, 4).reshape(nb, bs, H, Dx * x)
+    v = value_cache.transpose(0, 3, 1, 2)
+    return np.ascontiguousarray(k), np.ascontiguousarray(v)
+
+
+def paged_attention_xpacked(q: np.ndarray, key_cache: np.ndarray, value_cache: np.ndarray,
+                            block_tables: np.ndarray, seq_lens: np.ndarray, scale: float,
+                            dtype: str = "fp16", partition: int = 512):
+    """vLLM paged_attention_v1/v2 over the x-packed layout
+    (paged_transformer.py:325-332): out[b, h] = softmax(scale q.K^T) V over
+    the seq_lens[b] tokens of block_tables[b], kv head = h // (H / Hkv), in
+    fp32.  Also returns v2's per-partition scratch: max_logits[b, h, p] (max
+    scaled logit of the 512-token partition), exp_sums[b, h, p] (sum of
+    exp(logit - max)) and tmp_out[b, h, p] (the partition's normalised
+    output), fp32.  q: element bits [B, H, D]."""
+    qf = elem_to_f32(q, dtype)
+    B, Hq, D = qf.shape
+    kn, vn = xpacked_to_nhd(key_cache, value_cache)
+    Kf = elem_to_f32(kn, dtype)
+    Vf = elem_to_f32(vn, dtype)
+    bs, Hkv = kn.shape[1], kn.shape[2]
+    G = Hq // Hkv
+    P = max(1, max((int(n) + partition - 1) // partition for n in seq_lens))
+    out = np.zeros((B, Hq, D), np.float32)
+    ml = np.full((B, Hq, P), -np.inf, np.float32)
+    es = np.zeros((B, Hq, P), np.float32)
+    tmp = np.zeros((B, Hq, P, D), np.float32)
+    for b in range(B):
+        n = int(seq_lens[b])
+        if n == 0:
+            continue
+        pages = block_tables[b, :(n + bs - 1) // bs]
+        K = Kf[pages].reshape(-1, Hkv, D)[:n]
+        V = Vf[pages].reshape(-1, Hkv, D)[:n]
+        for h in range(Hq):
+            s = (K[:, h // G] @ qf[b, h]) * np.float32(scale)
+            e = np.exp(s - s.max())
+            out[b, h] = (e @ V[:, h // G]) / e.sum()
+            for p0 in range(0, n, partition):
+                sp = s[p0:p0 + partition]
+                ep = np.exp(sp - sp.max())
+                ml[b, h, p0 // partition] = sp.max()
+                es[b, h, p0 // partition] = ep.sum()
+                tmp[b, h, p0 // partition] = (ep @ V[p0:p0 + partition, h // G]) / ep.sum()
+    return out, ml, es, tmp
+
+
 # ---------------------------------------------------------------- swap
 
 

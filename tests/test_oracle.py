@@ -385,3 +385,73 @@ def test_paged_prefill_edge_cases():
     # request 2: q_len == kv_len -- plain causal, query 0 sees key 0 only
     V2 = orc.bf16_to_f32(vc)[bt[2, 0], :4]
     assert np.array_equal(out[3], V2[0][[0, 0, 1, 1]])
+
+
+# ------------------------------------------------- x-packed layout (f3)
+def test_xpacked_append_is_a_relayout_of_the_flat_append():
+    """Appending the same tokens to both layouts: the x-packed caches, read
+    through the closed-form transpose, equal the flat NHD caches; and a
+    hand-placed element lands where vLLM's layout puts it."""
+    rng = np.random.default_rng(50)
+    H, D, nb = 3, 16, 6
+    n = 40
+    key = rng.integers(0, 1 << 16, (n, H, D), dtype=np.uint16)
+    val = rng.integers(0, 1 << 16, (n, H, D), dtype=np.uint16)
+    slots = rng.permutation(nb * 16)[:n].astype(np.int64)
+    slots[3] = -1
+    kx = np.zeros((nb, H, D // 8, 16, 8), np.uint16)
+    vx = np.zeros((nb, H, D, 16), np.uint16)
+    orc.reshape_and_cache_xpacked(key, val, kx, vx, slots)
+    kf = np.zeros((nb, 16, H, D), np.uint16)
+    vf = np.zeros_like(kf)
+    orc.reshape_and_cache(key, val, kf, vf, slots)
+    kn, vn = orc.xpacked_to_nhd(kx, vx)
+    assert np.array_equal(kn, kf) and np.array_equal(vn, vf)
+    i, h, d = 7, 2, 13
+    blk, off = divmod(int(slots[i]), 16)
+    assert kx[blk, h, d // 8, off, d % 8] == key[i, h, d]
+    assert vx[blk, h, d, off] == val[i, h, d]
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (8, 2)])
+def test_xpacked_attention_matches_sdpa_and_partitions_merge(hq, hkv):
+    rng = np.random.default_rng(51)
+    D, nb = 128, 160
+    lens = [1, 300, 1100, 512, 17]
+    bt = np.full((len(lens), 70), -1, np.int32)
+    perm = rng.permutation(nb)
+    at = 0
+    for b, n in enumerate(lens):
+        k = (n + 15) // 16
+        bt[b, :k] = perm[at:at + k]
+        at += k
+    f16 = lambda a: a.astype(np.float16).view(np.uint16)
+    kx = f16(rng.standard_normal((nb, hkv, D // 8, 16, 8)))
+    vx = f16(rng.standard_normal((nb, hkv, D, 16)))
+    q = f16(rng.standard_normal((len(lens), hq, D)))
+    scale = 1 / np.sqrt(D)
+    out, ml, es, tmp = orc.paged_attention_xpacked(q, kx, vx, bt, np.array(lens), scale)
+    # torch SDPA on the same fp16 values (fp32 math), through the transpose
+    kn, vn = orc.xpacked_to_nhd(kx, vx)
+    K = torch.from_numpy(orc.elem_to_f32(kn, "fp16"))
+    V = torch.from_numpy(orc.elem_to_f32(vn, "fp16"))
+    qf = torch.from_numpy(orc.elem_to_f32(q, "fp16"))
+    for b, n in enumerate(lens):
+        pages = torch.from_numpy(bt[b, :(n + 15) // 16].astype(np.int64))
+        Kb = K[pages].flatten(0, 1)[:n].transpose(0, 1).contiguous()
+        Vb = V[pages].flatten(0, 1)[:n].transpose(0, 1).contiguous()
+        ref = torch.nn.functional.scaled_dot_product_attention(qf[b][:, None], Kb, Vb,
+                                                               enable_gqa=True)[:, 0]
+        assert np.abs(out[b] - ref.numpy()).max() < 3e-5
+    # vLLM's v2 reduce of the partitions gives the whole-sequence answer
+    for b, n in enumerate(lens):
+        P = (n + 511) // 512
+        M = ml[b, :, :P].max(axis=1, keepdims=True)
+        w = es[b, :, :P] * np.exp(ml[b, :, :P] - M)
+        red = (w[..., None] * tmp[b, :, :P]).sum(1) / w.sum(1, keepdims=True)
+        assert np.abs(red - out[b]).max() < 3e-5
+        assert np.isneginf(ml[b, :, P:]).all()
+    # a planted mistake -- the key's 16-byte chunks read in reverse order -- is caught
+    wrong, *_ = orc.paged_attention_xpacked(q, np.ascontiguousarray(kx[:, :, ::-1]), vx, bt,
+                                            np.array(lens), scale)
+    assert np.abs(wrong - out).max() > 1e-2
