@@ -12,10 +12,12 @@
 //   q.k : lane (token t = l%16, chunk group cg = l/16) loads the 16-byte
 //         chunks 4cg..4cg+3 of token t (dims 32cg..32cg+31), 16 dot2 per query
 //         head, then two xor-shuffles sum the 4 chunk groups;
-//   p.v : lane l loads dims 2l and 2l+1 over the page's 16 tokens (64 B);
-//         p is rounded to the cache dtype in (t, t+1) pairs -- as vLLM's kernel
-//         does before its value dot -- broadcast with v_readlane and folded
-//         with 8 dot2 per dim.
+//   p.v : lane l loads 16 B at 16l + 1024j (dim l/2 + 32j, tokens 8(l%2) ..
+//         +7; every load one contiguous KB); p is rounded to the cache dtype
+//         in (t, t+1) pairs -- as vLLM's kernel does before its value dot --
+//         broadcast with v_readlane and folded with 4 dot2 per dim; lanes l
+//         and l^1 add their token halves at the end.
+// Block ids are loaded 64 pages at a time, one per lane, and broadcast.
 // A workgroup (4 waves) owns one KV head x one 512-token partition (v2) or the
 // whole sequence (v1); wave w takes pages w, w+4, ...; the waves' softmax
 // states are merged through LDS.  v2 leaves vLLM's per-partition max logit,
@@ -77,31 +79,51 @@ struct XAppendArgs {
   int64_t block_stride;    // elements between cache blocks (K and V)
   int64_t head_stride;     // elements between heads of a block (K and V)
   int64_t num_slots;
+  int64_t num_tokens;
   int32_t num_heads;
   int32_t* oob_count;
 };
 
-// One workgroup per token; thread j copies 16-byte chunk j of the token's
-// K row (chunk c of head h lands on key_cache[blk][h][c][off][0..7], the
-// same 8 elements) and scatters 8 elements of its V row to
-// value_cache[blk][h][d][off].
+// Workgroup = 16 consecutive tokens x one head; thread (t, c) = (j/16, j%16)
+// reads 16-byte chunk c of token t's K and V rows (coalesced: 16 threads per
+// 256-byte row).  K chunk c of the token lands on key_cache[blk][h][c][off]
+// whole.  V goes to value_cache[blk][h][d][off], one element per dim; when
+// the 16 tokens fill one block in order (prefill), the workgroup transposes V
+// through LDS and writes each dim's 16 tokens as whole 16-byte runs,
+// otherwise (scattered decode slots) it stores the 8 elements one by one.
 __global__ __launch_bounds__(kThreads) void xpacked_append_kernel(XAppendArgs a) {
-  const int64_t i = blockIdx.x;
-  const int64_t slot = a.slots[i];
-  if (slot < 0) return;
-  if (slot >= a.num_slots) {
-    if (a.oob_count && threadIdx.x == 0) atomicAdd(a.oob_count, 1);
-    return;
+  __shared__ __align__(16) uint16_t s_v[kBlock][kD + 8];
+  const int h = blockIdx.y;
+  const int t = threadIdx.x >> 4, c = threadIdx.x & 15;
+  const int64_t i0 = int64_t(blockIdx.x) * kBlock;
+  const int64_t i = i0 + t;
+  const int64_t slot = i < a.num_tokens ? a.slots[i] : -1;
+  const int64_t slot0 = a.slots[i0];
+  const bool in_range = slot >= 0 && slot < a.num_slots;
+  const bool whole = __syncthreads_and(in_range && slot0 % kBlock == 0 && slot == slot0 + t);
+  if (slot >= a.num_slots && h == 0 && c == 0 && a.oob_count) atomicAdd(a.oob_count, 1);
+  uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+  if (in_range) {
+    kv = *reinterpret_cast<const uint4*>(a.key + i * a.key_stride + int64_t(h) * kD + c * kX);
+    vv = *reinterpret_cast<const uint4*>(a.value + i * a.value_stride + int64_t(h) * kD + c * kX);
   }
   const int64_t blk = slot / kBlock;
   const int off = int(slot % kBlock);
-  const int chunks = a.num_heads * (kD / kX);
-  for (int j = threadIdx.x; j < chunks; j += kThreads) {
-    const int h = j / (kD / kX), c = j % (kD / kX);
-    const uint4 kv = *reinterpret_cast<const uint4*>(a.key + i * a.key_stride + int64_t(j) * kX);
-    const uint4 vv = *reinterpret_cast<const uint4*>(a.value + i * a.value_stride + int64_t(j) * kX);
-    const int64_t base = blk * a.block_stride + int64_t(h) * a.head_stride;
-    *reinterpret_cast<uint4*>(a.key_cache + base + (int64_t(c) * kBlock + off) * kX) = kv;
+  const int64_t base = blk * a.block_stride + int64_t(h) * a.head_stride;
+  if (in_range)
+    store_stream(a.key_cache + base + (int64_t(c) * kBlock + off) * kX, kv);
+  if (whole) {
+    *reinterpret_cast<uint4*>(&s_v[t][c * kX]) = vv;
+    __syncthreads();
+    // thread j: dim j/2, tokens 8(j%2) .. +7 of the block
+    const int d = threadIdx.x >> 1, tb = 8 * (threadIdx.x & 1);
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = uint32_t(s_v[tb + 2 * e][d]) | (uint32_t(s_v[tb + 2 * e + 1][d]) << 16);
+    const int64_t base0 = (slot0 / kBlock) * a.block_stride + int64_t(h) * a.head_stride;
+    store_stream(a.value_cache + base0 + int64_t(d) * kBlock + tb, make_uint4(w[0], w[1], w[2], w[3]));
+  } else if (in_range) {
     uint16_t* vdst = a.value_cache + base + int64_t(c) * kX * kBlock + off;
     const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
@@ -154,36 +176,52 @@ __global__ __launch_bounds__(kThreads) void xpacked_decode_kernel(XDecodeArgs a)
       qw[g][4 * i] = v.x; qw[g][4 * i + 1] = v.y; qw[g][4 * i + 2] = v.z; qw[g][4 * i + 3] = v.w;
     }
   }
-  float m[G], l[G], acc[G][2];
+  float m[G], l[G], acc[G][4];  // acc[g][j]: dim lane/2 + 32j, half of the tokens
 #pragma unroll
-  for (int g = 0; g < G; ++g) { m[g] = kNegBig; l[g] = 0.f; acc[g][0] = acc[g][1] = 0.f; }
+  for (int g = 0; g < G; ++g) {
+    m[g] = kNegBig;
+    l[g] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[g][j] = 0.f;
+  }
 
   const int p_begin = t_begin / kBlock, p_end = (t_end + kBlock - 1) / kBlock;
   const int32_t* bt = a.block_tables + int64_t(b) * a.bt_stride;
-  struct Regs { uint4 k[4], v[4]; };
-  auto block_of = [&](int p) __attribute__((always_inline)) {
-    const int32_t id = p < a.bt_cols ? bt[p] : -1;
-    return (id >= 0 && id < a.num_blocks) ? id : -1;
+  // This wave's pages: p_begin + wave + 4j, j < n_pages.  Their block ids
+  // are loaded 64 at a time, one per lane, and broadcast with v_readlane.
+  const int first = p_begin + wave;
+  const int n_pages = p_end > first ? (p_end - first + kWaves - 1) / kWaves : 0;
+  int32_t id_reg = -1;
+  auto id_at = [&](int jj) __attribute__((always_inline)) {
+    if ((jj & 63) == 0) {
+      const int p = first + kWaves * (jj + lane);
+      const int32_t id = (jj + lane < n_pages && p < a.bt_cols) ? bt[p] : -1;
+      id_reg = (id >= 0 && id < a.num_blocks) ? id : -1;
+    }
+    return __builtin_amdgcn_readlane(id_reg, jj & 63);
   };
+  // V of a (block, head) is [D][16 tokens]; lane l loads bytes 16l + 1024j,
+  // i.e. dim l/2 + 32j, tokens 8(l%2) .. +7 -- one contiguous KB per load.
+  struct Regs { uint4 k[4], v[4]; };
+  const int vt0 = 8 * (lane & 1);
   auto load = [&](Regs& r, int32_t id) __attribute__((always_inline)) {
     const int64_t base = int64_t(id < 0 ? 0 : id) * a.block_stride + int64_t(h) * a.head_stride;
     const uint16_t* kb = a.k_cache + base + (int64_t(4 * cg) * kBlock + t) * kX;
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.k[i] = load_stream(kb + i * kBlock * kX);
-    const uint16_t* vb = a.v_cache + base + lane * 2 * kBlock;
+    const uint16_t* vb = a.v_cache + base + lane * kX;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r.v[j] = load_stream(vb + j * kX);
+    for (int j = 0; j < 4; ++j) r.v[j] = load_stream(vb + j * 64 * kX);
   };
   auto consume = [&](Regs& r, int p, int32_t id) __attribute__((always_inline)) {
     const int valid = id < 0 ? 0 : min(kBlock, t_end - p * kBlock);
+    uint32_t* vw = reinterpret_cast<uint32_t*>(r.v);  // [dim j][token pair k]
     if (valid < kBlock) {
       // tokens past the end: zero their V halves (they may hold NaN bits)
-      uint32_t* vw = reinterpret_cast<uint32_t*>(r.v);
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const int tok = 2 * (k & 7);
-        const uint32_t keep = (tok < valid ? 0xffffu : 0u) | (tok + 1 < valid ? 0xffff0000u : 0u);
-        vw[k] &= keep;
+      for (int w = 0; w < 16; ++w) {
+        const int tok = vt0 + 2 * (w & 3);
+        vw[w] &= (tok < valid ? 0xffffu : 0u) | (tok + 1 < valid ? 0xffff0000u : 0u);
       }
     }
     const bool live = t < valid;
@@ -205,50 +243,55 @@ __global__ __launch_bounds__(kThreads) void xpacked_decode_kernel(XDecodeArgs a)
       const float alpha = fast_exp2(m[g] - m_new);
       l[g] = fmaf(l[g], alpha, row16_sum(pr));
       m[g] = m_new;
-      // (p[t], p[t+1]) as one element pair in even lanes, broadcast
+      // (p[t], p[t+1]) as one element pair in even lanes, broadcast; this
+      // lane needs the pairs of tokens vt0 .. vt0+7.
       const float nxt = __shfl_down(pr, 1, 16);
       const uint32_t pair = to_elem<kBf16>(pr) | (to_elem<kBf16>(nxt) << 16);
-      uint32_t pw[8];
+      uint32_t pw[4];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) pw[k] = __builtin_amdgcn_readlane(pair, 2 * k);
-      const uint32_t* vw = reinterpret_cast<const uint32_t*>(r.v);
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t lo = __builtin_amdgcn_readlane(pair, 2 * k);
+        const uint32_t hi = __builtin_amdgcn_readlane(pair, 8 + 2 * k);
+        pw[k] = vt0 ? hi : lo;
+      }
 #pragma unroll
-      for (int dd = 0; dd < 2; ++dd) {
-        float o = acc[g][dd] * alpha;
+      for (int j = 0; j < 4; ++j) {
+        float o = acc[g][j] * alpha;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) o = dot2<kBf16>(pw[k], vw[8 * dd + k], o);
-        acc[g][dd] = o;
+        for (int k = 0; k < 4; ++k) o = dot2<kBf16>(pw[k], vw[4 * j + k], o);
+        acc[g][j] = o;
       }
     }
   };
 
-  // Two register stages: page p + 4 is in flight while page p is consumed.
+  // Two register stages: the wave's next page is in flight while one is consumed.
   Regs ra, rb;
-  int p = p_begin + wave;
-  int32_t ida = p < p_end ? block_of(p) : -1;
-  if (p < p_end) load(ra, ida);
-  for (; p < p_end; p += 2 * kWaves) {
-    const int pb = p + kWaves;
-    int32_t idb = -1;
-    if (pb < p_end) { idb = block_of(pb); load(rb, idb); }
-    consume(ra, p, ida);
-    if (pb >= p_end) break;
-    const int pa = pb + kWaves;
-    if (pa < p_end) { ida = block_of(pa); load(ra, ida); }
-    consume(rb, pb, idb);
+  int32_t ida = -1, idb = -1;
+  if (n_pages > 0) { ida = id_at(0); load(ra, ida); }
+  for (int j = 0; j < n_pages; j += 2) {
+    if (j + 1 < n_pages) { idb = id_at(j + 1); load(rb, idb); }
+    consume(ra, first + kWaves * j, ida);
+    if (j + 1 >= n_pages) break;
+    if (j + 2 < n_pages) { ida = id_at(j + 2); load(ra, ida); }
+    consume(rb, first + kWaves * (j + 1), idb);
   }
+  // the two token halves of each dim live in lanes l and l^1
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[g][j] += __shfl_xor(acc[g][j], 1);
 
-  // Merge the 4 waves' states (lane l holds dims 2l, 2l+1 of every head).
+  // Merge the 4 waves' states.
   __shared__ float s_m[kWaves][G], s_l[kWaves][G];
   __shared__ float s_acc[kWaves][G][kD];
   if (lane == 0)
 #pragma unroll
     for (int g = 0; g < G; ++g) { s_m[wave][g] = m[g]; s_l[wave][g] = l[g]; }
+  if ((lane & 1) == 0)
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    s_acc[wave][g][2 * lane] = acc[g][0];
-    s_acc[wave][g][2 * lane + 1] = acc[g][1];
-  }
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s_acc[wave][g][(lane >> 1) + 32 * j] = acc[g][j];
   __syncthreads();
   // Thread j < G*D: head g = j / D, dim d = j % D.
   for (int j = threadIdx.x; j < G * kD; j += kThreads) {
@@ -437,10 +480,11 @@ extern "C" int kvc_reshape_and_cache_xpacked(
   a.block_stride = cache_block_stride;
   a.head_stride = cache_head_stride;
   a.num_slots = num_blocks * kBlock;
+  a.num_tokens = num_tokens;
   a.num_heads = num_heads;
   a.oob_count = oob_count;
-  xpacked_append_kernel<<<dim3(unsigned(num_tokens)), kThreads, 0,
-                          static_cast<hipStream_t>(stream)>>>(a);
+  xpacked_append_kernel<<<dim3(unsigned((num_tokens + kBlock - 1) / kBlock), unsigned(num_heads)),
+                          kThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
   KVC_LAUNCH_CHECK();
   return ok();
 }
