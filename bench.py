@@ -20,8 +20,8 @@ merge kernel, bracketed by HIP events on the stream they run on) against the
 8 TB/s HBM3E peak.  ``extra`` carries the other rows of the metric: chunked-
 prefill append and gather GB/s (configuration 3), long-context decode GB/s
 (configuration 4), swap host-link GB/s with decode slowdown
-(configuration 5) and continuation-prefill TFLOP/s (the MFMA attention after
-the configuration 3 append).  ``cpu_baseline`` times the numpy oracle on one layer of
+(configuration 5), continuation-prefill TFLOP/s (the MFMA attention after
+the configuration 3 append) and the x-packed layout's decode / append GB/s.  ``cpu_baseline`` times the numpy oracle on one layer of
 the same workload on the host cores.
 
 Other modes used by the profiles (one kernel family each, few launches):
@@ -31,6 +31,9 @@ Other modes used by the profiles (one kernel family each, few launches):
   --mode append3  configuration 3 append + gather, one layer, 10 launches each
   --mode prefill3 continuation prefill after the cfg3 append (8 x 2048-token
                   chunks over 2048 and 4096 cached tokens), 10 launches each
+  --mode xpacked  vLLM x-packed layout: paged_attention_v2 (1 x 150K and
+                  64 x U[512,4096] tokens, MHA 32 x 128 fp16) and
+                  reshape_and_cache, 10 launches each
 """
 from __future__ import annotations
 
@@ -77,7 +80,8 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip configurations 3-5")
     p.add_argument("--mode", default="step",
-                   choices=["step", "copy", "decode2", "decode4", "append3", "prefill3"])
+                   choices=["step", "copy", "decode2", "decode4", "append3", "prefill3",
+                            "xpacked"])
     return p.parse_args()
 
 
@@ -374,6 +378,91 @@ def run_prefill(torch, seed, reps=10):
     return res
 
 
+def run_xpacked(torch, seed, reps=10):
+    """vLLM x-packed layout (the reference's dense sandbox): paged_attention_v2
+    at the shape of the reference's GH200 data point -- one 150,000-token
+    decode, 32 MHA heads x 128, fp16, 16-token blocks in random order
+    (src/dense/include/paged_transformer.py:103-111, 325-332) -- and a 64-
+    sequence batch with context U[512, 4096]; reshape_and_cache of a
+    16,384-token prefill (whole blocks) and of a 64-token decode step
+    (scattered slots)."""
+    import numpy as np
+
+    from gpu_offloading_amd import ops
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 21)
+    h, d = 32, 128
+    res = {}
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = _events(torch)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / reps
+
+    rng = np.random.default_rng(seed + 22)
+    for name, lens in (("v2_1x150000", [150000]),
+                       ("v2_64xU512_4096", rng.integers(512, 4097, 64).tolist())):
+        need = sum((n + 15) // 16 for n in lens)
+        nb = need + 16
+        kc = torch.empty(nb, h, d // 8, 16, 8, dtype=torch.float16, device="cuda")
+        vc = torch.empty(nb, h, d, 16, dtype=torch.float16, device="cuda")
+        kc.normal_(0, 1, generator=g)
+        vc.normal_(0, 1, generator=g)
+        perm = torch.randperm(nb, generator=g, device="cuda").to(torch.int32)
+        bt = torch.full((len(lens), max((n + 15) // 16 for n in lens)), -1, dtype=torch.int32,
+                        device="cuda")
+        at = 0
+        for b, n in enumerate(lens):
+            k = (n + 15) // 16
+            bt[b, :k] = perm[at:at + k]
+            at += k
+        q = torch.randn(len(lens), h, d, device="cuda", generator=g).to(torch.float16)
+        sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+        msl = max(lens)
+        parts = (msl + 511) // 512
+        out = torch.empty_like(q)
+        es = torch.empty(len(lens), h, parts, device="cuda")
+        ml = torch.empty_like(es)
+        tmp = torch.empty(len(lens), h, parts, d, dtype=q.dtype, device="cuda")
+        t = timed(lambda: ops.paged_attention_v2(out, es, ml, tmp, q, kc, vc, h, d ** -0.5, bt, sl,
+                                                 16, msl, None, "auto", 1.0, 1.0, 0, 0, 0, 0, 0))
+        byts = sum(lens) * h * d * 2 * 2 + 2 * len(lens) * h * d * 2
+        assert torch.isfinite(out).all().item(), "non-finite v2 output"
+        res[name] = {"us": t * 1e6, "GBps": byts / t / 1e9, "frac_of_peak": byts / t / 1e9 / HBM_PEAK_GBPS,
+                     "algorithmic_bytes": byts, "seqs": len(lens), "tokens": int(sum(lens))}
+        log(f"x-packed {name}: {t * 1e6:.1f} us, {byts / t / 1e9:.0f} GB/s "
+            f"({byts / t / 1e9 / HBM_PEAK_GBPS:.1%} of peak)")
+        del kc, vc, q, out, es, ml, tmp, bt
+        torch.cuda.empty_cache()
+    # reshape_and_cache: K/V are views of a packed qkv [N, 3, H, D] (the sandbox's layout)
+    n = 16384
+    nb = n // 16 + 64
+    kc = torch.zeros(nb, h, d // 8, 16, 8, dtype=torch.float16, device="cuda")
+    vc = torch.zeros(nb, h, d, 16, dtype=torch.float16, device="cuda")
+    qkv = torch.randn(n, 3, h, d, device="cuda", generator=g).to(torch.float16)
+    blocks = torch.randperm(nb, generator=g, device="cuda")[: n // 16]
+    slots = (blocks.repeat_interleave(16) * 16 + torch.arange(16, device="cuda").repeat(n // 16)).long()
+    t = timed(lambda: ops.reshape_and_cache(qkv[:, 1], qkv[:, 2], kc, vc, slots))
+    byts = n * (2 * h * d * 2 * 2 + 8)
+    res["append_prefill_16384"] = {"us": t * 1e6, "GBps": byts / t / 1e9,
+                                   "frac_of_peak": byts / t / 1e9 / HBM_PEAK_GBPS}
+    dec = slots[::256][:64].contiguous()
+    t64 = timed(lambda: ops.reshape_and_cache(qkv[:64, 1], qkv[:64, 2], kc, vc, dec))
+    res["append_decode_64_us"] = t64 * 1e6
+    log(f"x-packed reshape_and_cache: 16384 tokens {t * 1e6:.1f} us = {byts / t / 1e9:.0f} GB/s; "
+        f"64 scattered tokens {t64 * 1e6:.1f} us")
+    del kc, vc, qkv
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_cfg4(torch, seed, reps=32):
     from gpu_offloading_amd import workloads
 
@@ -589,6 +678,9 @@ def main():
     if args.mode == "decode4":
         run_cfg4(torch, args.seed)
         return
+    if args.mode == "xpacked":
+        print(json.dumps({"mode": "xpacked", **run_xpacked(torch, args.seed)}), flush=True)
+        return
     if args.mode == "prefill3":
         print(json.dumps({"mode": "prefill3", **run_prefill(torch, args.seed)}), flush=True)
         return
@@ -603,6 +695,7 @@ def main():
         extra["cfg4_long_context"] = run_cfg4(torch, args.seed)
         extra["cfg5_swap"] = run_cfg5(torch, args.seed)
         extra["f2_continuation_prefill"] = run_prefill(torch, args.seed)
+        extra["f3_xpacked"] = run_xpacked(torch, args.seed)
     cpu = None if args.no_cpu else run_cpu_baseline(args.seed)
     line = {
         "metric": "paged decode-attn HBM GB/s (% peak) + KV append/gather/swap GB/s, 1 GPU",

@@ -33,7 +33,7 @@ namespace {
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
-constexpr int kWaves = 4;
+constexpr int kV2Waves = 4;  // waves per v2 workgroup (1, 2 and 4 measured alike)
 constexpr int kBlock = 16;    // tokens per block
 constexpr int kD = 128;       // head size
 constexpr int kX = 8;         // elements per 16-byte chunk
@@ -155,9 +155,14 @@ struct XDecodeArgs {
   uint16_t* tmp_out;       // [seqs][H][max_parts][D]
 };
 
-template <int G, bool kBf16, bool kV1>
-__global__ __launch_bounds__(kThreads) void xpacked_decode_kernel(XDecodeArgs a) {
-  const int part = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+template <int G, bool kBf16, bool kV1, int kW>
+__global__ __launch_bounds__(64 * kW) void xpacked_decode_kernel(XDecodeArgs a) {
+  // Grid (KV head, sequence, partition): consecutive workgroups -- which the
+  // dispatcher deals to different XCDs -- are heads of one (sequence,
+  // partition), i.e. equal work.  (Partition-fastest order put every
+  // sequence's partition p on XCD p % 8 and left the XCDs of the late,
+  // mostly absent, partitions idle: 4.7 -> 6+ TB/s on a 64-sequence batch.)
+  const int h = blockIdx.x, b = blockIdx.y, part = blockIdx.z;
   const int seq_len = max(a.seq_lens[b], 0);
   const int t_begin = kV1 ? 0 : part * kPart;
   const int t_end = kV1 ? seq_len : min(seq_len, t_begin + kPart);
@@ -190,11 +195,11 @@ __global__ __launch_bounds__(kThreads) void xpacked_decode_kernel(XDecodeArgs a)
   // This wave's pages: p_begin + wave + 4j, j < n_pages.  Their block ids
   // are loaded 64 at a time, one per lane, and broadcast with v_readlane.
   const int first = p_begin + wave;
-  const int n_pages = p_end > first ? (p_end - first + kWaves - 1) / kWaves : 0;
+  const int n_pages = p_end > first ? (p_end - first + kW - 1) / kW : 0;
   int32_t id_reg = -1;
   auto id_at = [&](int jj) __attribute__((always_inline)) {
     if ((jj & 63) == 0) {
-      const int p = first + kWaves * (jj + lane);
+      const int p = first + kW * (jj + lane);
       const int32_t id = (jj + lane < n_pages && p < a.bt_cols) ? bt[p] : -1;
       id_reg = (id >= 0 && id < a.num_blocks) ? id : -1;
     }
@@ -270,10 +275,10 @@ __global__ __launch_bounds__(kThreads) void xpacked_decode_kernel(XDecodeArgs a)
   if (n_pages > 0) { ida = id_at(0); load(ra, ida); }
   for (int j = 0; j < n_pages; j += 2) {
     if (j + 1 < n_pages) { idb = id_at(j + 1); load(rb, idb); }
-    consume(ra, first + kWaves * j, ida);
+    consume(ra, first + kW * j, ida);
     if (j + 1 >= n_pages) break;
     if (j + 2 < n_pages) { ida = id_at(j + 2); load(ra, ida); }
-    consume(rb, first + kWaves * (j + 1), idb);
+    consume(rb, first + kW * (j + 1), idb);
   }
   // the two token halves of each dim live in lanes l and l^1
 #pragma unroll
@@ -282,8 +287,8 @@ __global__ __launch_bounds__(kThreads) void xpacked_decode_kernel(XDecodeArgs a)
     for (int j = 0; j < 4; ++j) acc[g][j] += __shfl_xor(acc[g][j], 1);
 
   // Merge the 4 waves' states.
-  __shared__ float s_m[kWaves][G], s_l[kWaves][G];
-  __shared__ float s_acc[kWaves][G][kD];
+  __shared__ float s_m[kW][G], s_l[kW][G];
+  __shared__ float s_acc[kW][G][kD];
   if (lane == 0)
 #pragma unroll
     for (int g = 0; g < G; ++g) { s_m[wave][g] = m[g]; s_l[wave][g] = l[g]; }
@@ -294,14 +299,14 @@ __global__ __launch_bounds__(kThreads) void xpacked_decode_kernel(XDecodeArgs a)
       for (int j = 0; j < 4; ++j) s_acc[wave][g][(lane >> 1) + 32 * j] = acc[g][j];
   __syncthreads();
   // Thread j < G*D: head g = j / D, dim d = j % D.
-  for (int j = threadIdx.x; j < G * kD; j += kThreads) {
+  for (int j = threadIdx.x; j < G * kD; j += 64 * kW) {
     const int g = j / kD, d = j % kD;
     float mx = kNegBig;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][g]);
+    for (int w = 0; w < kW; ++w) mx = fmaxf(mx, s_m[w][g]);
     float L = 0.f, O = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < kW; ++w) {
       const float sc = fast_exp2(s_m[w][g] - mx);
       L = fmaf(s_l[w][g], sc, L);
       O = fmaf(s_acc[w][g][d], sc, O);
@@ -323,38 +328,84 @@ __global__ __launch_bounds__(kThreads) void xpacked_decode_kernel(XDecodeArgs a)
 
 // v2 reduce (vLLM's rule): M = max_p max_logits[p], w_p = exp_sums[p] *
 // exp(max_logits[p] - M), out = sum_p w_p tmp_out[p] / sum_p w_p.  One
-// partition: out = tmp_out[0].
+// partition: out = tmp_out[0].  Workgroup = (query head, sequence), 256
+// threads: the partitions' weights are computed in chunks of 256 into LDS,
+// then thread (dim d, half r) sums every other partition of the chunk with
+// four loads in flight, and the halves are added through LDS.
+constexpr int kRedThreads = 256;
 template <bool kBf16>
-__global__ __launch_bounds__(kD) void xpacked_reduce_kernel(XDecodeArgs a) {
-  const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+__global__ __launch_bounds__(kRedThreads) void xpacked_reduce_kernel(XDecodeArgs a) {
+  __shared__ float s_w[kRedThreads];
+  __shared__ float s_part[kRedThreads / 64];
+  __shared__ float s_o[2][kD];
+  const int hq = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int Hq = gridDim.x;
   const int seq_len = max(a.seq_lens[b], 0);
   const int parts = min((seq_len + kPart - 1) / kPart, a.grid_parts);
   const int64_t row = (int64_t(b) * Hq + hq) * a.max_parts;
-  uint16_t* dst = a.out + (int64_t(b) * Hq + hq) * kD + d;
+  uint16_t* dst = a.out + (int64_t(b) * Hq + hq) * kD;
   if (parts <= 1) {
-    *dst = parts == 1 ? a.tmp_out[row * kD + d] : uint16_t(0);
+    if (tid < kD) dst[tid] = parts == 1 ? a.tmp_out[row * kD + tid] : uint16_t(0);
     return;
   }
+  // global max logit
   float mx = -INFINITY;
-  for (int p = 0; p < parts; ++p) mx = fmaxf(mx, a.max_logits[row + p]);
-  float S = 0.f, O = 0.f;
-  for (int p = 0; p < parts; ++p) {
-    const float lg = a.max_logits[row + p];
-    const float w = lg == -INFINITY ? 0.f : a.exp_sums[row + p] * fast_exp2((lg - mx) * kLog2e);
-    S += w;
-    O = fmaf(w, from_elem<kBf16>(a.tmp_out[(row + p) * kD + d]), O);
+  for (int p = tid; p < parts; p += kRedThreads) mx = fmaxf(mx, a.max_logits[row + p]);
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  if ((tid & 63) == 0) s_part[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(s_part[0], s_part[1]), fmaxf(s_part[2], s_part[3]));
+  const int d = tid & (kD - 1), r = tid >> 7;  // two halves of 128 threads
+  float O[2] = {0.f, 0.f}, S = 0.f;
+  for (int c0 = 0; c0 < parts; c0 += kRedThreads) {
+    __syncthreads();  // s_w of the previous chunk is consumed
+    {
+      const int p = c0 + tid;
+      float w = 0.f;
+      if (p < parts) {
+        const float lg = a.max_logits[row + p];
+        w = lg == -INFINITY ? 0.f : a.exp_sums[row + p] * fast_exp2((lg - mx) * kLog2e);
+      }
+      s_w[tid] = w;
+      S += w;
+    }
+    __syncthreads();
+    const int n = min(kRedThreads, parts - c0);
+    const uint16_t* src = a.tmp_out + (row + c0) * kD + d;
+    int p = r;
+    for (; p + 6 < n; p += 8) {  // four partitions per half in flight
+      const float v0 = from_elem<kBf16>(src[int64_t(p) * kD]);
+      const float v1 = from_elem<kBf16>(src[int64_t(p + 2) * kD]);
+      const float v2 = from_elem<kBf16>(src[int64_t(p + 4) * kD]);
+      const float v3 = from_elem<kBf16>(src[int64_t(p + 6) * kD]);
+      O[0] = fmaf(s_w[p], v0, O[0]);
+      O[1] = fmaf(s_w[p + 2], v1, O[1]);
+      O[0] = fmaf(s_w[p + 4], v2, O[0]);
+      O[1] = fmaf(s_w[p + 6], v3, O[1]);
+    }
+    for (; p < n; p += 2) O[0] = fmaf(s_w[p], from_elem<kBf16>(src[int64_t(p) * kD]), O[0]);
   }
-  *dst = uint16_t(to_elem<kBf16>(S > 0.f ? O / S : 0.f));
+  // sum of weights over the workgroup, and the two halves' outputs
+  for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off);
+  __syncthreads();
+  if ((tid & 63) == 0) s_part[tid >> 6] = S;
+  s_o[r][d] = O[0] + O[1];
+  __syncthreads();
+  if (tid < kD) {
+    const float tot = s_part[0] + s_part[1] + s_part[2] + s_part[3];
+    const float o = s_o[0][tid] + s_o[1][tid];
+    dst[tid] = uint16_t(to_elem<kBf16>(tot > 0.f ? o / tot : 0.f));
+  }
 }
 
 template <int G, bool kBf16>
 void launch_decode(const XDecodeArgs& a, bool v1, int parts, int hkv, int seqs, hipStream_t s) {
   if (v1) {
-    xpacked_decode_kernel<G, kBf16, true><<<dim3(1, hkv, seqs), kThreads, 0, s>>>(a);
+    xpacked_decode_kernel<G, kBf16, true, 4><<<dim3(hkv, seqs, 1), 256, 0, s>>>(a);
   } else {
-    xpacked_decode_kernel<G, kBf16, false><<<dim3(parts, hkv, seqs), kThreads, 0, s>>>(a);
-    xpacked_reduce_kernel<kBf16><<<dim3(hkv * G, seqs), kD, 0, s>>>(a);
+    xpacked_decode_kernel<G, kBf16, false, kV2Waves>
+        <<<dim3(hkv, seqs, parts), 64 * kV2Waves, 0, s>>>(a);
+    xpacked_reduce_kernel<kBf16><<<dim3(hkv * G, seqs), kRedThreads, 0, s>>>(a);
   }
 }
 
@@ -402,6 +453,8 @@ int paged_attention(bool v1, void* out, float* exp_sums, float* max_logits, void
                   kv_head_stride % 8 == 0,
               KVC_ERR_ALIGNMENT, "query/cache pointers and strides must be 16-byte aligned");
   const int parts = (max_seq_len + kPart - 1) / kPart;
+  KVC_REQUIRE(num_seqs <= 65535 && parts <= 65535, KVC_ERR_INVALID_ARG,
+              "at most 65535 sequences and 65535 partitions per call");
   if (!v1) {
     KVC_REQUIRE(exp_sums && max_logits && tmp_out, KVC_ERR_INVALID_ARG,
                 "v2 needs exp_sums, max_logits and tmp_out");
