@@ -21,7 +21,8 @@ merge kernel, bracketed by HIP events on the stream they run on) against the
 prefill append and gather GB/s (configuration 3), long-context decode GB/s
 (configuration 4), swap host-link GB/s with decode slowdown
 (configuration 5), continuation-prefill TFLOP/s (the MFMA attention after
-the configuration 3 append) and the x-packed layout's decode / append GB/s.  ``cpu_baseline`` times the numpy oracle on one layer of
+the configuration 3 append), the x-packed layout's decode / append GB/s, and
+the host-memory policies (layer-wise offload pipeline, swap preemption).  ``cpu_baseline`` times the numpy oracle on one layer of
 the same workload on the host cores.
 
 Other modes used by the profiles (one kernel family each, few launches):
@@ -34,6 +35,8 @@ Other modes used by the profiles (one kernel family each, few launches):
   --mode xpacked  vLLM x-packed layout: paged_attention_v2 (1 x 150K and
                   64 x U[512,4096] tokens, MHA 32 x 128 fp16) and
                   reshape_and_cache, 10 launches each
+  --mode offload  layer-wise KV offload pipeline (8 layers, 25% of blocks in
+                  host memory) and swap preemption of a 4096-token request
 """
 from __future__ import annotations
 
@@ -81,7 +84,7 @@ def parse_args():
     p.add_argument("--no-extra", action="store_true", help="skip configurations 3-5")
     p.add_argument("--mode", default="step",
                    choices=["step", "copy", "decode2", "decode4", "append3", "prefill3",
-                            "xpacked"])
+                            "xpacked", "offload"])
     return p.parse_args()
 
 
@@ -463,6 +466,113 @@ def run_xpacked(torch, seed, reps=10):
     return res
 
 
+def run_offload(torch, seed, steps=3):
+    """Host-memory KV policies.  (a) Layer-wise offload of the dense sandbox
+    (paged_offload_transformer.py): 8 layers, MHA 32 x 128 fp16, a mixed
+    batch of 32 decodes over 2048-token histories + 2 prefills of 512 tokens,
+    25% of every sequence's blocks in pinned host memory for layers 1..7,
+    staged through two scratchpads by the three-stream pipeline; per step
+    each layer appends and runs paged_attention_v2.  Reported: step time,
+    the same step all-resident, and the host-link rate of the staging.
+    (b) Swap preemption, Mixtral-shaped (32 layers, Hkv 8, D 128, bf16): one
+    4096-token request swapped out and back in."""
+    from gpu_offloading_amd import ops
+    from gpu_offloading_amd.kv_cache import PagedKVCache
+    from gpu_offloading_amd.offload import KVOffloadPipeline, PagedOffloadKV, SwapPreemption
+
+    res = {}
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 31)
+    L, H = 8, 32
+    dec, pre = [2048] * 32, [512] * 2
+    for ratio in (0.0, 0.25):
+        kv = PagedOffloadKV(dec, pre, L, H, 128, ratio, device="cuda", allocation_mode="random",
+                            seed=seed + 32)
+        kv.key_heap.normal_(0, 1, generator=g)
+        kv.val_heap.normal_(0, 1, generator=g)
+        for t in kv.k_offload_cpu + kv.v_offload_cpu:
+            t.normal_(0, 1)
+        pipe = KVOffloadPipeline(kv) if ratio > 0 else None
+        T = kv.total_tokens
+        ks = [torch.randn(T, H, 128, device="cuda", generator=g).half() for _ in range(L)]
+        qs = [torch.randn(len(dec), H, 128, device="cuda", generator=g).half() for _ in range(L)]
+        out = torch.empty_like(qs[0])
+
+        def step():
+            if pipe:
+                pipe.begin_step()
+            for layer in range(L):
+                if pipe:
+                    pipe.before_append(layer)
+                ops.reshape_and_cache(ks[layer], ks[layer], kv.key_heap, kv.val_heap,
+                                      kv.slot_mapping[layer])
+                if pipe:
+                    pipe.prefill_done(layer)
+                    pipe.before_decode(layer)
+                ops.paged_attention_v2(out, kv.exp_sums, kv.max_logits, kv.tmp_output, qs[layer],
+                                       kv.key_heap, kv.val_heap, H, 0.0884,
+                                       kv.decode_block_table(layer), kv.decode_context_lens, 16,
+                                       kv.max_decode_len)
+                if pipe:
+                    pipe.layer_done(layer)
+
+        step()
+        torch.cuda.synchronize()
+        if pipe:
+            pipe.synchronize()
+            pipe.copy_seconds()
+            pipe.h2d_bytes = pipe.d2h_bytes = 0
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        if pipe:
+            pipe.synchronize()
+        wall = (time.perf_counter() - t0) / steps
+        r = {"kv_offload_ratio": ratio, "step_ms": wall * 1e3}
+        if pipe:
+            cs = pipe.copy_seconds()
+            r.update({"h2d_GB_per_step": pipe.h2d_bytes / steps / 1e9,
+                      "h2d_GBps": pipe.h2d_bytes / cs["h2d"] / 1e9,
+                      "d2h_GBps": pipe.d2h_bytes / cs["d2h"] / 1e9 if cs["d2h"] else None,
+                      "link_bound_step_ms": cs["h2d"] / steps * 1e3})
+        res[f"layer_offload_ratio_{ratio}"] = r
+        log(f"offload ratio {ratio}: step {wall * 1e3:.2f} ms" +
+            (f", H2D {r['h2d_GB_per_step']:.2f} GB/step at {r['h2d_GBps']:.1f} GB/s "
+             f"(copy-stream time {r['link_bound_step_ms']:.2f} ms/step), "
+             f"D2H {r['d2h_GBps']:.1f} GB/s" if pipe else ""))
+        del kv, pipe, ks, qs, out
+        torch.cuda.empty_cache()
+
+    cache = PagedKVCache(32, 8, 128, max_seqs=4, max_seq_len=4096 + 64, num_qo_heads=32,
+                         kv_page_budget=600, device="cuda", workspace_bytes=1 << 24,
+                         staging_bytes=256 << 20)
+    cache.ensure_pages(0, 256)
+    cache.advance([0], [4096])
+    for layer in range(32):
+        cache.k_cache[layer].normal_(0, 1, generator=g)
+    pre = SwapPreemption(cache)
+    snap = cache.k_cache[5][cache.block_table[0, :256].long()].clone()
+    torch.cuda.synchronize()
+    h = pre.preempt(0, key="r0")
+    cache.synchronize_swaps()
+    t_out = h.out_seconds()
+    pre.resume("r0", slot=1)
+    cache.synchronize_swaps()
+    t_in = h.in_seconds()
+    exact = bool(torch.equal(cache.k_cache[5][cache.block_table[1, :256].long()], snap))
+    res["swap_preemption_4096_tokens"] = {
+        "bytes_each_way": h.num_bytes, "out_ms": t_out * 1e3, "in_ms": t_in * 1e3,
+        "out_GBps": h.num_bytes / t_out / 1e9, "in_GBps": h.num_bytes / t_in / 1e9,
+        "restored_exact": exact}
+    log(f"swap preemption of a 4096-token request (32 layers): out {t_out * 1e3:.1f} ms "
+        f"({h.num_bytes / t_out / 1e9:.1f} GB/s), in {t_in * 1e3:.1f} ms "
+        f"({h.num_bytes / t_in / 1e9:.1f} GB/s), restored exact {exact}")
+    del cache
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_cfg4(torch, seed, reps=32):
     from gpu_offloading_amd import workloads
 
@@ -678,6 +788,9 @@ def main():
     if args.mode == "decode4":
         run_cfg4(torch, args.seed)
         return
+    if args.mode == "offload":
+        print(json.dumps({"mode": "offload", **run_offload(torch, args.seed)}), flush=True)
+        return
     if args.mode == "xpacked":
         print(json.dumps({"mode": "xpacked", **run_xpacked(torch, args.seed)}), flush=True)
         return
@@ -696,6 +809,7 @@ def main():
         extra["cfg5_swap"] = run_cfg5(torch, args.seed)
         extra["f2_continuation_prefill"] = run_prefill(torch, args.seed)
         extra["f3_xpacked"] = run_xpacked(torch, args.seed)
+        extra["f4_offload"] = run_offload(torch, args.seed)
     cpu = None if args.no_cpu else run_cpu_baseline(args.seed)
     line = {
         "metric": "paged decode-attn HBM GB/s (% peak) + KV append/gather/swap GB/s, 1 GPU",

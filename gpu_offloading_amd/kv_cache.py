@@ -578,21 +578,27 @@ class PagedKVCache:
         self._pending_free.append((ev, ids, [ids_t, host]))
         return SwapHandle(seq_ids, lens, npages, ids_t, host, ev, out_start=start, num_bytes=nbytes)
 
-    def swap_in(self, handle: SwapHandle, wait: bool = False) -> None:
+    def swap_in(self, handle: SwapHandle, wait: bool = False,
+                seq_ids: Optional[Sequence[int]] = None) -> None:
         """Restore an evicted handle into freshly allocated pages.
 
         Allocation and block-table updates happen now; the H2D copies and the
         scatter run on the side stream after everything already enqueued on
         the current stream.  Later ``plan_decode`` / ``gather`` / ``swap_out``
         of these sequences make the current stream wait for the restore;
-        ``wait=True`` does so immediately."""
+        ``wait=True`` does so immediately.  ``seq_ids`` restores into other
+        (non-resident) sequence slots, one per evicted sequence, in order --
+        a preempted request may resume in whatever slot is free."""
         self._require_gpu()
         self._require_dynamic()
         if handle.restored:
             raise RuntimeError("swap handle already restored")
+        targets = list(handle.seq_ids) if seq_ids is None else [int(s) for s in seq_ids]
+        if len(targets) != len(handle.seq_ids) or len(set(targets)) != len(targets):
+            raise ValueError("seq_ids must name one distinct slot per evicted sequence")
         cur = torch.cuda.current_stream(self.device)
         dst = []
-        for sid, n, ln in zip(handle.seq_ids, handle.num_pages, handle.seq_lens):
+        for sid, n, ln in zip(targets, handle.num_pages, handle.seq_lens):
             if self._pool.seq_pages(sid) != 0 or int(self._seq_lens_cpu[sid]) != 0:
                 raise RuntimeError(f"seq {sid} is resident; free it before swap_in")
             self.alloc_pages(sid, n)
@@ -610,7 +616,8 @@ class PagedKVCache:
         handle.in_event = ev
         handle.dst_block_ids = dst_t
         handle.restored = True
-        for sid in handle.seq_ids:
+        handle.seq_ids = targets
+        for sid in targets:
             self._pending_in[sid] = ev
         if wait:
-            self._sync_seqs(handle.seq_ids)
+            self._sync_seqs(targets)

@@ -1,0 +1,136 @@
+"""GPU tests of the host-memory KV policies: layer-wise offload through two
+scratchpads and three streams gives bit-identical attention to the all-
+resident layout and writes the new prefill blocks back exactly; swap-based
+preemption resumes a request with bit-identical decode outputs."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_offloading_amd import ops, workloads
+from gpu_offloading_amd.kv_cache import PagedKVCache
+from gpu_offloading_amd.offload import KVOffloadPipeline, PagedOffloadKV, SwapPreemption
+
+pytestmark = pytest.mark.gpu
+
+
+def _step(kv, pipe, ks, vs, qs):
+    """One mixed step over all layers (append, then decode attention);
+    returns the per-layer decode outputs."""
+    outs = []
+    if pipe:
+        pipe.begin_step()
+    for layer in range(kv.num_layers):
+        if pipe:
+            pipe.before_append(layer)
+        ops.reshape_and_cache(ks[layer], vs[layer], kv.key_heap, kv.val_heap,
+                              kv.slot_mapping[layer])
+        if pipe:
+            pipe.prefill_done(layer)
+            pipe.before_decode(layer)
+        q = qs[layer]
+        out = torch.empty_like(q)
+        ops.paged_attention_v2(out, kv.exp_sums, kv.max_logits, kv.tmp_output, q, kv.key_heap,
+                               kv.val_heap, kv.num_heads, 0.0884, kv.decode_block_table(layer),
+                               kv.decode_context_lens, 16, kv.max_decode_len)
+        if pipe:
+            pipe.layer_done(layer)
+        outs.append(out)
+    torch.cuda.synchronize()
+    if pipe:
+        pipe.synchronize()
+    return [o.clone() for o in outs]
+
+
+@pytest.mark.parametrize("ratio,mode", [(0.5, "random"), (0.9, "contiguous")])
+def test_offload_pipeline_matches_resident_layout(gpu, ratio, mode):
+    dec, pre, L, H = [100, 37, 300, 64, 1], [40, 17], 5, 4
+    off = PagedOffloadKV(dec, pre, L, H, 128, ratio, device=gpu, allocation_mode=mode, seed=3)
+    res = PagedOffloadKV(dec, pre, L, H, 128, 0.0, device=gpu, allocation_mode="random", seed=4)
+    assert off.decode_offload_blocks > 0 and off.prefill_offload_blocks > 0
+    g = torch.Generator(device=gpu).manual_seed(70)
+    for layer in range(L):
+        for i, n in enumerate(dec):
+            k = torch.randn(n, H, 128, generator=g, device=gpu).half()
+            v = torch.randn(n, H, 128, generator=g, device=gpu).half()
+            off.load_history(layer, i, k, v)
+            res.load_history(layer, i, k, v)
+    pipe = KVOffloadPipeline(off)
+    for step in range(2):   # the second step reuses both scratchpads
+        T = off.total_tokens
+        ks = [torch.randn(T, H, 128, generator=g, device=gpu).half() for _ in range(L)]
+        vs = [torch.randn(T, H, 128, generator=g, device=gpu).half() for _ in range(L)]
+        qs = [torch.randn(len(dec), H, 128, generator=g, device=gpu).half() for _ in range(L)]
+        got = _step(off, pipe, ks, vs, qs)
+        want = _step(res, None, ks, vs, qs)
+        for layer in range(L):
+            assert torch.equal(got[layer], want[layer]), (step, layer)
+        # the prefill sequences' offloaded blocks went back to host memory
+        for layer in range(1, L):
+            for b in range(len(pre)):
+                n_off = off.offload_counts[b]
+                o = off.scratchpad_seq_offsets[b] - off.decode_offload_blocks
+                ids = res.block_tables_cpu[layer, b, :n_off].long().to(gpu)
+                assert torch.equal(off.k_prefill_cpu[layer - 1][o:o + n_off].to(gpu), res.key_heap[ids])
+                assert torch.equal(off.v_prefill_cpu[layer - 1][o:o + n_off].to(gpu), res.val_heap[ids])
+    t = pipe.copy_seconds()
+    assert pipe.h2d_bytes > 0 and t["h2d"] > 0
+
+
+def test_swap_preemption_resumes_bit_identically(gpu):
+    """Four sequences decode for 8 steps; in the tight pool the scheduler
+    preempts the last one at step 2 (swap) and resumes it at step 5 in
+    another slot.  The reference pool pauses it in place.  Every decode
+    output matches bit for bit."""
+    L, Hkv, Hq = 2, 8, 32
+    kw = dict(num_qo_heads=Hq, device=gpu, workspace_bytes=1 << 24, staging_bytes=1 << 22)
+    tight = PagedKVCache(L, Hkv, 128, max_seqs=6, max_seq_len=640, kv_page_budget=110,
+                         free_page_order=workloads.randperm(110, 71), **kw)
+    ample = PagedKVCache(L, Hkv, 128, max_seqs=6, max_seq_len=640, kv_page_budget=400,
+                         free_page_order=workloads.randperm(400, 72), **kw)
+    g = torch.Generator(device=gpu).manual_seed(73)
+    lens = [300, 450, 500, 420]
+    for cache in (tight, ample):
+        g2 = torch.Generator(device=gpu).manual_seed(74)
+        for s, n in enumerate(lens):
+            cache.ensure_pages(s, (n + 15) // 16)
+        slots = cache.slot_mapping(range(4), lens)
+        for layer in range(L):
+            k = torch.randn(sum(lens), Hkv, 128, generator=g2, device=gpu).to(torch.bfloat16)
+            v = torch.randn(sum(lens), Hkv, 128, generator=g2, device=gpu).to(torch.bfloat16)
+            cache.append(layer, k, v, slots)
+        cache.advance(range(4), lens)
+    pre = SwapPreemption(tight)
+    where = {0: 0, 1: 1, 2: 2, 3: 3}   # request -> slot in the tight cache
+    used_before = tight.pages_in_use
+    for step in range(8):
+        if step == 2:
+            pre.preempt(where.pop(3), key=3)
+            tight.synchronize_swaps()
+            assert tight.pages_in_use == used_before - (lens[3] + 15) // 16
+        if step == 5:
+            where[3] = 5                   # resumes in another free slot
+            assert pre.pages_to_resume(3) == (lens[3] + 2 + 15) // 16   # 2 steps decoded
+            assert pre.swapped_len(3) == lens[3] + 2
+            pre.resume(3, slot=5)
+        active = sorted(where)             # requests decoding this step
+        k = [torch.randn(len(active), Hkv, 128, generator=g, device=gpu).to(torch.bfloat16)
+             for _ in range(L)]
+        v = [torch.randn(len(active), Hkv, 128, generator=g, device=gpu).to(torch.bfloat16)
+             for _ in range(L)]
+        q = [torch.randn(len(active), Hq, 128, generator=g, device=gpu).to(torch.bfloat16)
+             for _ in range(L)]
+        outs = {}
+        for name, cache, slot_of in (("tight", tight, where), ("ample", ample, {r: r for r in where})):
+            seqs = [slot_of[r] for r in active]
+            for s in seqs:
+                cache.ensure_pages(s, (int(cache._seq_lens_cpu[s]) + 1 + 15) // 16)
+            slots = cache.prepare_decode_step(seqs)
+            res = []
+            for layer in range(L):
+                cache.append(layer, k[layer], v[layer], slots)
+                res.append(cache.decode(layer, q[layer]))
+            torch.cuda.synchronize()
+            outs[name] = res
+        for layer in range(L):
+            assert torch.equal(outs["tight"][layer], outs["ample"][layer]), (step, layer)
+    assert pre.swaps_out == 1 and pre.swaps_in == 1 and not pre.is_swapped(3)
