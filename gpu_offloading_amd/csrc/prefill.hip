@@ -161,16 +161,32 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   const int64_t tok_bytes = a.token_stride * 2;
 
   uint4 kreg[4], vreg[4];
+  // Page ids of a tile, fetched one iteration before its K/V loads need them
+  // (four independent loads at clamped addresses; validity applied after),
+  // so no load waits on an id.
+  // Nothing reads the loaded ids until load_tile, so no wait sits here;
+  // which of them exist is decided from the page index alone.
+  struct TileIds { int32_t v[4]; int exists; };
+  auto fetch_ids = [&](int tile) __attribute__((always_inline)) {
+    TileIds t;
+    t.exists = 0;
+    const int64_t last = a.num_indices - 1;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = tile * 4 + u;
+      t.v[u] = a.indices[min(int64_t(page_off) + p, last)];
+      t.exists |= (p < npages && int64_t(page_off) + p <= last) ? (1 << u) : 0;
+    }
+    return t;
+  };
   // load_tile returns a mask whose bit u says page u of the tile is real.
-  auto load_tile = [&](int tile) __attribute__((always_inline)) {
+  auto load_tile = [&](const TileIds& t) __attribute__((always_inline)) {
     int ok = 0;
     int32_t ids[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int p = tile * 4 + u;
-      int32_t id = -1;
-      if (p < npages && int64_t(page_off) + p < a.num_indices) id = a.indices[page_off + p];
-      const bool good = id >= 0 && id < a.num_blocks;
+      const int32_t id = __builtin_amdgcn_readfirstlane(t.v[u]);
+      const bool good = ((t.exists >> u) & 1) && id >= 0 && id < a.num_blocks;
       ok |= good ? (1 << u) : 0;
       ids[u] = good ? id : 0;
     }
@@ -317,10 +333,16 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   const bool all_pages = __syncthreads_and(bad == 0);
   const int lim_lo = a.causal ? tok0 + kv_len - q_len : kv_len - 1;
   const int n_full = all_pages ? max(0, min(ntiles, (lim_lo + 1) / kKeys)) : 0;
+  // Per iteration: K/V loads of tile+1 (ids fetched last iteration), id
+  // fetch of tile+2, the tile's math, staging of tile+1, one barrier.
+  TileIds ids_next;
   auto run_tiles = [&](int t0, int t1, int ok, auto masked) __attribute__((always_inline)) {
     for (int tile = t0; tile < t1; ++tile) {
       int next_ok = 0;
-      if (tile + 1 < ntiles) next_ok = load_tile(tile + 1);
+      if (tile + 1 < ntiles) {
+        next_ok = load_tile(ids_next);
+        if (tile + 2 < ntiles) ids_next = fetch_ids(tile + 2);
+      }
       compute(tiles[tile & 1], tile, ok, masked);
       if (tile + 1 < ntiles) stage_tile(tiles[(tile + 1) & 1], tile + 1, next_ok);
       ok = next_ok;
@@ -329,7 +351,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
     return ok;
   };
   if (ntiles > 0) {
-    int ok = load_tile(0);
+    int ok = load_tile(fetch_ids(0));
+    if (ntiles > 1) ids_next = fetch_ids(1);
     stage_tile(tiles[0], 0, ok);
     __syncthreads();
     ok = run_tiles(0, n_full, ok, std::false_type{});
@@ -448,7 +471,8 @@ extern "C" int kvc_batch_prefill_run(const kvc_prefill_schedule* sched, const in
   if (sched->num_items == 0) return ok();
   KVC_REQUIRE(plan && q && key_cache && value_cache && out && indices, KVC_ERR_INVALID_ARG,
               "null pointer");
-  KVC_REQUIRE(num_blocks > 0 && num_indices >= 0, KVC_ERR_INVALID_ARG, "bad num_blocks");
+  KVC_REQUIRE(num_blocks > 0 && num_indices > 0, KVC_ERR_INVALID_ARG,
+              "bad num_blocks or empty indices");
   KVC_REQUIRE(cache_token_stride >= int64_t(Hkv) * kD && cache_block_stride >= cache_token_stride * kPage,
               KVC_ERR_INVALID_ARG, "cache strides smaller than the block");
   KVC_REQUIRE(q_token_stride >= int64_t(Hq) * kD && out_token_stride >= int64_t(Hq) * kD,
