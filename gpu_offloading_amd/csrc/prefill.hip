@@ -159,6 +159,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   const char* vbase = reinterpret_cast<const char*>(a.v_cache);
   const int64_t blk_bytes = a.block_stride * 2;
   const int64_t tok_bytes = a.token_stride * 2;
+  const uint32_t k_lane_off = uint32_t(k_tok * tok_bytes + (head_off + k_chunk * 8) * 2);
 
   uint4 kreg[4], vreg[4];
   // Page ids of a tile, fetched one iteration before its K/V loads need them
@@ -191,9 +192,10 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
       ids[u] = good ? id : 0;
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      kreg[u] = *reinterpret_cast<const uint4*>(kbase + int64_t(ids[u]) * blk_bytes +
-                                                k_tok * tok_bytes + (head_off + k_chunk * 8) * 2);
+    for (int u = 0; u < 4; ++u) {
+      const char* blk = kbase + int64_t(ids[u]) * blk_bytes;  // uniform
+      kreg[u] = *reinterpret_cast<const uint4*>(blk + k_lane_off);
+    }
     int32_t vid = ids[0];
 #pragma unroll
     for (int u = 1; u < 4; ++u) vid = v_page == u ? ids[u] : vid;
@@ -203,24 +205,31 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
       vreg[e] = *reinterpret_cast<const uint4*>(vp + (v_tok + e) * tok_bytes);
     return ok;
   };
+  // Keys past the cache or in a missing page are staged as zeros: a mask
+  // (v_and) on tiles that have such keys, nothing on the others.
   auto stage_tile = [&](TileBuf& buf, int tile, int ok) __attribute__((always_inline)) {
     const int key0 = tile * kKeys;
+    if (ok != 0xF || key0 + kKeys > kv_len) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int key = u * kPage + k_tok;
-      const bool live = ((ok >> u) & 1) && key0 + key < kv_len;
-      *reinterpret_cast<uint4*>(buf.k + key * kKPitch + k_chunk * 16) =
-          live ? kreg[u] : make_uint4(0, 0, 0, 0);
-    }
-    // V: zero the keys that do not exist, then write 8 dims x 4 keys transposed.
-    uint32_t w[4][4];
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t m = (((ok >> u) & 1) && key0 + u * kPage + k_tok < kv_len) ? ~0u : 0u;
+        kreg[u].x &= m; kreg[u].y &= m; kreg[u].z &= m; kreg[u].w &= m;
+      }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int key = v_page * kPage + v_tok + e;
-      const bool live = ((ok >> v_page) & 1) && key0 + key < kv_len;
-      const uint4 v = live ? vreg[e] : make_uint4(0, 0, 0, 0);
-      w[e][0] = v.x; w[e][1] = v.y; w[e][2] = v.z; w[e][3] = v.w;
+      for (int e = 0; e < 4; ++e) {
+        const int key = v_page * kPage + v_tok + e;
+        const uint32_t m = (((ok >> v_page) & 1) && key0 + key < kv_len) ? ~0u : 0u;
+        vreg[e].x &= m; vreg[e].y &= m; vreg[e].z &= m; vreg[e].w &= m;
+      }
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      *reinterpret_cast<uint4*>(buf.k + (u * kPage + k_tok) * kKPitch + k_chunk * 16) = kreg[u];
+    // V: 8 dims x 4 keys written transposed.
+    const uint32_t w[4][4] = {{vreg[0].x, vreg[0].y, vreg[0].z, vreg[0].w},
+                              {vreg[1].x, vreg[1].y, vreg[1].z, vreg[1].w},
+                              {vreg[2].x, vreg[2].y, vreg[2].z, vreg[2].w},
+                              {vreg[3].x, vreg[3].y, vreg[3].z, vreg[3].w}};
     const int key = v_page * kPage + v_tok;
     uint8_t* dst = buf.vt + (v_chunk * 8) * kVPitch + vt_pos(key) * 2;
 #pragma unroll
@@ -475,6 +484,8 @@ extern "C" int kvc_batch_prefill_run(const kvc_prefill_schedule* sched, const in
               "bad num_blocks or empty indices");
   KVC_REQUIRE(cache_token_stride >= int64_t(Hkv) * kD && cache_block_stride >= cache_token_stride * kPage,
               KVC_ERR_INVALID_ARG, "cache strides smaller than the block");
+  KVC_REQUIRE(cache_token_stride * kPage * 2 < (int64_t(1) << 31), KVC_ERR_INVALID_ARG,
+              "a cache block spans more than 2 GiB");
   KVC_REQUIRE(q_token_stride >= int64_t(Hq) * kD && out_token_stride >= int64_t(Hq) * kD,
               KVC_ERR_INVALID_ARG, "q/out token stride smaller than Hq*head_dim");
   KVC_REQUIRE(sm_scale > 0.f, KVC_ERR_INVALID_ARG, "sm_scale must be positive");
