@@ -19,6 +19,7 @@ from __future__ import annotations
 import math
 from typing import Optional, Tuple, Union
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -174,6 +175,45 @@ class BatchDecodeWithPagedKVCacheWrapper:
         self._plan_args = (batch, num_qo_heads, num_kv_heads, head_dim, page_size)
 
     begin_forward = plan
+
+    # ------------------------------------------------- in-package fast path
+    def _plan_capacity(self, batch: int) -> int:
+        """int32 entries to reserve for the plan image (16-byte multiple)."""
+        cap = _lib.load().kvc_decode_plan_ints(batch, max(self._segments_hint, 8 * self._num_cus))
+        return (cap + 3) // 4 * 4
+
+    def _schedule_into(self, indptr_host: np.ndarray, lpl_host: np.ndarray, batch: int,
+                       num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
+                       image: torch.Tensor) -> _lib.KvcDecodeSchedule:
+        """kvc_decode_plan into the pinned int32 ``image``.  If the image is
+        too small, the returned schedule's ``plan_ints`` exceeds
+        ``image.numel()`` and nothing is staged: retry with a larger one."""
+        sched = _lib.KvcDecodeSchedule()
+        st = _lib.load().kvc_decode_plan(indptr_host.ctypes.data, lpl_host.ctypes.data, batch,
+                                         num_qo_heads, num_kv_heads, head_dim, page_size,
+                                         self._segments_hint, self._num_cus, sched,
+                                         image.data_ptr(), image.numel())
+        if st == _lib.KVC_ERR_WORKSPACE and sched.plan_ints > image.numel():
+            return sched
+        _lib.check("kvc_decode_plan", st)
+        ws = self._workspace.numel() * self._workspace.element_size()
+        if sched.workspace_bytes > ws:
+            _fail(f"decode workspace too small: need {sched.workspace_bytes} bytes, have {ws}")
+        return sched
+
+    def _install(self, sched: _lib.KvcDecodeSchedule, plan_dev: torch.Tensor,
+                 indptr_dev: torch.Tensor, lpl_dev: torch.Tensor, indices_dev: torch.Tensor,
+                 num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int) -> None:
+        """Adopt a schedule whose image and metadata are already on the device
+        (staged by the caller in stream order before the next ``run``)."""
+        self._sched = sched
+        self._plan_dev = plan_dev
+        self._indptr = indptr_dev
+        self._lpl = lpl_dev
+        self._indices = indices_dev
+        self._num_indices = indices_dev.numel()
+        self._sm_scale = 1.0 / math.sqrt(head_dim)
+        self._plan_args = (sched.batch, num_qo_heads, num_kv_heads, head_dim, page_size)
 
     @property
     def schedule(self) -> _lib.KvcDecodeSchedule:

@@ -106,11 +106,15 @@ class PagedKVCache:
         self.v_cache = [torch.zeros(shape, dtype=dtype, device=self.device) for _ in range(num_layers)]
 
         if self._dynamic_pages:
-            self.block_table = torch.full((max_seqs, self.max_pages_per_seq), -1,
-                                          dtype=torch.int32, device=self.device)
+            self._bt = torch.full((max_seqs, self.max_pages_per_seq), -1,
+                                  dtype=torch.int32, device=self.device)
         else:
-            self.block_table = torch.arange(max_seqs * self.max_pages_per_seq, dtype=torch.int32,
-                                            device=self.device).view(max_seqs, self.max_pages_per_seq)
+            self._bt = torch.arange(max_seqs * self.max_pages_per_seq, dtype=torch.int32,
+                                    device=self.device).view(max_seqs, self.max_pages_per_seq)
+        # Block-table writes of a GPU cache wait here (flat position -> page
+        # id, last write wins) until the next decode step uploads them with
+        # the rest of its metadata, or ``block_table`` is read.
+        self._bt_pending: dict[int, int] = {}
         self.seq_lens = torch.zeros(max_seqs, dtype=torch.int32, device=self.device)
         self._seq_lens_cpu = torch.zeros(max_seqs, dtype=torch.int32)
         self._pool = PagePool(self.total_pages, max_seqs, self.max_pages_per_seq,
@@ -161,6 +165,43 @@ class PagedKVCache:
         else:
             self.seq_lens.copy_(self._seq_lens_cpu)
 
+    @property
+    def block_table(self) -> torch.Tensor:
+        """``[max_seqs, max_pages_per_seq]`` int32 physical page ids (-1 for
+        none), on the cache's device, with every earlier write applied."""
+        self._flush_block_table()
+        return self._bt
+
+    def _bt_write(self, seq_id: int, start: int, pages) -> None:
+        """``block_table[seq_id, start:start+len(pages)] = pages`` (an int or
+        a sequence), deferred on a GPU cache."""
+        if isinstance(pages, int):
+            raise TypeError("pages must be a sequence")
+        if self.device.type != "cuda":
+            self._bt[seq_id, start:start + len(pages)] = torch.as_tensor(pages, dtype=torch.int32)
+            return
+        base = seq_id * self.max_pages_per_seq + start
+        for j, p in enumerate(pages):
+            self._bt_pending[base + j] = int(p)
+
+    def _take_bt_pending(self):
+        """(positions int64, values int32) of the pending writes, cleared."""
+        if not self._bt_pending:
+            return None
+        pos = np.fromiter(self._bt_pending.keys(), dtype=np.int64, count=len(self._bt_pending))
+        val = np.fromiter(self._bt_pending.values(), dtype=np.int32, count=len(self._bt_pending))
+        self._bt_pending.clear()
+        return pos, val
+
+    def _flush_block_table(self) -> None:
+        pend = self._take_bt_pending()
+        if pend is None:
+            return
+        pos, val = pend
+        both = np.concatenate([pos, val.astype(np.int64)])
+        d = self._to_device(both)
+        self._bt.view(-1).scatter_(0, d[:len(pos)], d[len(pos):].to(torch.int32))
+
     def _require_gpu(self) -> None:
         if self._decode_wrapper is None:
             raise RuntimeError("this operation needs a GPU-resident PagedKVCache (device='cuda')")
@@ -188,17 +229,14 @@ class PagedKVCache:
             return
         self._reclaim(need=n_pages)
         current, pages = self._pool.alloc(seq_id, n_pages)
-        page_t = torch.tensor(pages, dtype=torch.int32)
-        if self.device.type == "cuda":
-            page_t = self._to_device(page_t)  # async: no host-GPU sync per allocation
-        self.block_table[seq_id, current:current + n_pages] = page_t
+        self._bt_write(seq_id, current, pages)
 
     def free_seq_pages(self, seq_id: int) -> None:
         """moe_engine.py:4261-4273: pages back to the free list, row -> -1."""
         self._require_dynamic()
         pages = self._pool.release(seq_id)
         if pages:
-            self.block_table[seq_id, :len(pages)] = -1
+            self._bt_write(seq_id, 0, [-1] * len(pages))
 
     def ensure_pages(self, seq_id: int, needed_pages: int) -> None:
         """moe_engine.py:4275-4283: grow seq_id to needed_pages (no-op if enough)."""
@@ -240,7 +278,8 @@ class PagedKVCache:
             vc.zero_()
         if self._dynamic_pages:
             self._pool.reset()
-            self.block_table.fill_(-1)
+            self._bt_pending.clear()
+            self._bt.fill_(-1)
         self._pending_free.clear()
         self._pending_in.clear()
 
@@ -386,11 +425,74 @@ class PagedKVCache:
         lengths, then ``seq_lens += 1``, then plan.  Pages must already cover
         the new token (the scheduler's ``ensure_pages``)."""
         self._require_gpu()
+        b = len(seq_ids)
+        graph_n = b if graph_n is None else graph_n
+        if b == 0 or graph_n < b:
+            # Nothing to plan, or an error for slot_mapping to report.
+            slots = self.slot_mapping(seq_ids, [1] * b, graph_n)
+            return slots
         self._sync_seqs(seq_ids)
-        slots = self.slot_mapping(seq_ids, [1] * len(seq_ids), graph_n)
-        self._seq_lens_cpu.numpy()[np.asarray(seq_ids, dtype=np.int64)] += 1
-        self._lens_to_device()
-        self.plan_decode(seq_ids)
+        ids = np.asarray(seq_ids, dtype=np.int64)
+        lens_all = self._seq_lens_cpu.numpy()
+        if len(np.unique(ids)) != b:
+            raise ValueError("seq_ids must be distinct")
+        ms, ps = self.max_seqs, self.page_size
+        lens = lens_all[ids].astype(np.int32) + 1
+
+        # One pinned int32 image of the step's metadata, one H2D copy:
+        #   ids[b] | qsl[b+1] | lens_before[ms] | lens_after[ms] | kv_indptr[b+1]
+        #   | last_page_len[b] | block-table positions (int64) | page ids
+        #   | decode schedule (16-byte aligned)
+        pend = self._take_bt_pending()
+        u = 0 if pend is None else len(pend[0])
+        w = self._decode_wrapper
+        o_ids, o_qsl = 0, b
+        o_lb = o_qsl + b + 1
+        o_la = o_lb + ms
+        o_ip = o_la + ms
+        o_lpl = o_ip + b + 1
+        o_pos = (o_lpl + b + 1) // 2 * 2
+        o_val = o_pos + 2 * u
+        o_plan = (o_val + u + 3) // 4 * 4
+        cap = w._plan_capacity(b)
+        while True:
+            hs = torch.empty(o_plan + cap, dtype=torch.int32, pin_memory=True)
+            h = hs.numpy()
+            h[o_ids:o_qsl] = ids
+            h[o_qsl:o_lb] = np.arange(b + 1, dtype=np.int32)
+            h[o_lb:o_la] = lens_all
+            h[o_la:o_ip] = lens_all
+            h[o_la + ids] += 1
+            nblk = (lens + ps - 1) // ps
+            h[o_ip] = 0
+            np.cumsum(nblk, out=h[o_ip + 1:o_ip + b + 1])
+            lpl = lens % ps
+            h[o_lpl:o_lpl + b] = np.where(lpl == 0, ps, lpl)
+            if u:
+                h[o_pos:o_pos + 2 * u].view(np.int64)[:] = pend[0]
+                h[o_val:o_val + u] = pend[1]
+            sched = w._schedule_into(h[o_ip:o_ip + b + 1], h[o_lpl:o_lpl + b], b,
+                                     self.num_heads, self.num_kv_heads, self.head_dim, ps,
+                                     hs[o_plan:])
+            if sched.plan_ints <= cap:
+                break
+            cap = (sched.plan_ints + 3) // 4 * 4
+        total = int(h[o_ip + b])
+        lens_all[ids] += 1
+
+        dm = hs.to(self.device, non_blocking=True)
+        if u:
+            self._bt.view(-1).scatter_(0, dm[o_pos:o_val].view(torch.int64), dm[o_val:o_val + u])
+        ids_d = dm[o_ids:o_qsl]
+        slots = torch.empty(graph_n, dtype=torch.int64, device=self.device)
+        ops.compute_slot_mapping(self._bt, ids_d, dm[o_qsl:o_lb], dm[o_lb:o_la], b, slots,
+                                 block_size=ps)
+        self.seq_lens.copy_(dm[o_la:o_ip])
+        indptr_d = dm[o_ip:o_lpl]
+        ops.copy_page_indices(self._bt, indptr_d, self._plan_indices_gpu, seq_ids=ids_d)
+        w._install(sched, dm[o_plan:o_plan + cap], indptr_d, dm[o_lpl:o_lpl + b],
+                   self._plan_indices_gpu[:total], self.num_heads, self.num_kv_heads,
+                   self.head_dim, ps)
         return slots
 
     # ------------------------------------------------------- per-layer ops
@@ -561,7 +663,7 @@ class PagedKVCache:
             npages.append(len(pages))
             ids.extend(pages)
             if pages:
-                self.block_table[sid, :len(pages)] = -1
+                self._bt_write(sid, 0, [-1] * len(pages))
             self._seq_lens_cpu[sid] = 0
         self._lens_to_device()
         n = len(ids)
