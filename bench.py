@@ -89,6 +89,24 @@ def parse_args():
 
 
 # --------------------------------------------------------------- helpers
+def _timed_rounds(torch, fn, reps, rounds=3):
+    """Median over ``rounds`` of the mean event time (s) of ``reps`` calls,
+    after a few untimed calls that bring the clocks up."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(rounds):
+        e0, e1 = _events(torch)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e-3 / reps)
+    return sorted(ts)[len(ts) // 2]
+
+
 def _events(torch):
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
@@ -193,7 +211,7 @@ def run_step_bench(torch, args):
         "value": step_gbps,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": profiled_traffic(),
-                     "kernel": "decode_lds_kernel<4> + decode_merge_kernel<128>",
+                     "kernel": "decode_lds_kernel<4, 8> + decode_merge_kernel<128>",
                      "avg_launch_us": avg_ms * 1e3, "algorithmic_bytes_per_launch": avg_bytes,
                      "segments": sched.num_segments, "head_groups": sched.num_head_groups,
                      "max_partitions": sched.max_partitions},
@@ -360,15 +378,7 @@ def run_prefill(torch, seed, reps=10):
                num_qo_heads=hq, num_kv_heads=hkv, head_dim_qk=d, page_size=16, causal=True,
                q_data_type=torch.bfloat16)
         out = torch.empty_like(q)
-        w.run(q, (kc, vc), out=out)
-        torch.cuda.synchronize()
-        e0, e1 = _events(torch)
-        e0.record()
-        for _ in range(reps):
-            w.run(q, (kc, vc), out=out)
-        e1.record()
-        torch.cuda.synchronize()
-        t = e0.elapsed_time(e1) * 1e-3 / reps
+        t = _timed_rounds(torch, lambda: w.run(q, (kc, vc), out=out), reps)
         f = prefill_flops(q_lens, kv_lens, hq, d)
         assert torch.isfinite(out).all().item(), "non-finite prefill output"
         res[name] = {"q_len": q_len, "kv_len": kv_len, "requests": 8, "us": t * 1e6,
@@ -399,15 +409,7 @@ def run_xpacked(torch, seed, reps=10):
     res = {}
 
     def timed(fn):
-        fn()
-        torch.cuda.synchronize()
-        e0, e1 = _events(torch)
-        e0.record()
-        for _ in range(reps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e-3 / reps
+        return _timed_rounds(torch, fn, reps)
 
     rng = np.random.default_rng(seed + 22)
     for name, lens in (("v2_1x150000", [150000]),
