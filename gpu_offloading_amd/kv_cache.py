@@ -561,9 +561,13 @@ class PagedKVCache:
         ``host`` ([layers][n][2][block_bytes]) through the two staging halves:
         gather/scatter kernels on the side stream, the host-link copies on the
         DMA stream, ordered by events, so that the copy of one chunk overlaps
-        the kernel of the next.  A half is reused only after its previous copy
-        (swap-out) or scatter (swap-in) completed.  Returns (start, end)
-        events; the side stream has already waited for the current stream."""
+        the kernels of the next.  A chunk fills a staging half with consecutive
+        (layer, block) items of the host image, across layer boundaries (one
+        kernel per layer it touches, one copy), so small swaps make few large
+        copies: each copy costs the DMA queue a fixed ~0.1-0.5 ms.  A half is
+        reused only after its previous copy (swap-out) or scatter (swap-in)
+        completed.  Returns (start, end) events; the side stream has already
+        waited for the current stream."""
         side, dma = self._side_stream(), self._dma_stream()
         bb = ops.block_bytes(self.k_cache[0])
         per = 2 * bb
@@ -573,41 +577,47 @@ class PagedKVCache:
         if not to_host:
             dma.wait_event(start)
         end = None
-        i = 0
-        for layer in range(self.num_layers):
-            for c0 in range(0, n, chunk):
-                c = min(chunk, n - c0)
-                b = i % 2
-                buf = halves[b][: c * per]
-                ids_c = ids_t[c0: c0 + c]
-                h0 = (layer * n + c0) * per
-                hview = host[h0: h0 + c * per]
-                done = torch.cuda.Event(enable_timing=True)
-                if to_host:
-                    if self._staging_free[b] is not None:
-                        side.wait_event(self._staging_free[b])
-                    ops.gather_blocks(self.k_cache[layer], self.v_cache[layer], ids_c, buf,
-                                      stream=side)
-                    gathered = torch.cuda.Event()
-                    gathered.record(side)
-                    dma.wait_event(gathered)
-                    with torch.cuda.stream(dma):
-                        hview.copy_(buf, non_blocking=True)
-                    done.record(dma)
-                else:
-                    if self._staging_free[b] is not None:
-                        dma.wait_event(self._staging_free[b])
-                    with torch.cuda.stream(dma):
-                        buf.copy_(hview, non_blocking=True)
-                    loaded = torch.cuda.Event()
-                    loaded.record(dma)
-                    side.wait_event(loaded)
-                    ops.scatter_blocks(buf, ids_c, self.k_cache[layer], self.v_cache[layer],
-                                       stream=side)
-                    done.record(side)
-                self._staging_free[b] = done
-                end = done
-                i += 1
+        total = self.num_layers * n
+        for i, f0 in enumerate(range(0, total, chunk)):
+            c = min(chunk, total - f0)
+            b = i % 2
+            buf = halves[b][: c * per]
+            hview = host[f0 * per: (f0 + c) * per]
+            # (layer, first block, end block, offset in the chunk) per layer touched
+            segs = []
+            f = f0
+            while f < f0 + c:
+                layer, j0 = divmod(f, n)
+                j1 = min(n, j0 + (f0 + c - f))
+                segs.append((layer, j0, j1, f - f0))
+                f += j1 - j0
+            done = torch.cuda.Event(enable_timing=True)
+            if to_host:
+                if self._staging_free[b] is not None:
+                    side.wait_event(self._staging_free[b])
+                for layer, j0, j1, o in segs:
+                    ops.gather_blocks(self.k_cache[layer], self.v_cache[layer], ids_t[j0:j1],
+                                      buf[o * per: (o + j1 - j0) * per], stream=side)
+                gathered = torch.cuda.Event()
+                gathered.record(side)
+                dma.wait_event(gathered)
+                with torch.cuda.stream(dma):
+                    hview.copy_(buf, non_blocking=True)
+                done.record(dma)
+            else:
+                if self._staging_free[b] is not None:
+                    dma.wait_event(self._staging_free[b])
+                with torch.cuda.stream(dma):
+                    buf.copy_(hview, non_blocking=True)
+                loaded = torch.cuda.Event()
+                loaded.record(dma)
+                side.wait_event(loaded)
+                for layer, j0, j1, o in segs:
+                    ops.scatter_blocks(buf[o * per: (o + j1 - j0) * per], ids_t[j0:j1],
+                                       self.k_cache[layer], self.v_cache[layer], stream=side)
+                done.record(side)
+            self._staging_free[b] = done
+            end = done
         ids_t.record_stream(side)
         if end is None:
             end = torch.cuda.Event(enable_timing=True)

@@ -127,3 +127,48 @@ def test_copy_page_indices_vs_oracle(gpu):
                           out, seq_ids=torch.tensor(seq_ids, dtype=torch.int32, device=gpu))
     got = out.cpu().numpy()
     assert np.array_equal(got[:-5], ref) and (got[-5:] == -7).all()
+
+
+@pytest.mark.parametrize("staging_blocks", [1, 3, 7, 1000])
+def test_cache_swap_chunks_across_layers_bit_exact(gpu, staging_blocks):
+    """PagedKVCache.swap_out / swap_in with staging halves of 1, 3, 7 and
+    1000 blocks: chunks pack consecutive (layer, block) items of the host
+    image across layer boundaries.  The host image equals the oracle's
+    layer-by-layer block image, and the restore into other slots is exact."""
+    from gpu_offloading_amd.kv_cache import PagedKVCache
+
+    layers, hkv = 3, 2
+    per = 2 * 16 * hkv * 128 * 2
+    cache = PagedKVCache(layers, hkv, 128, max_seqs=4, max_seq_len=256, kv_page_budget=64,
+                         free_page_order=workloads.randperm(64, 80), device=gpu,
+                         workspace_bytes=1 << 20, staging_bytes=2 * staging_blocks * per)
+    lens = {0: 70, 1: 40, 2: 64}
+    for s, ln in lens.items():
+        cache.ensure_pages(s, (ln + 15) // 16)
+    cache.advance(list(lens), list(lens.values()))
+    cache.fill_kv_random(1.0, generator=torch.Generator(device=gpu).manual_seed(81))
+    bt = cache.block_table.cpu().numpy()
+    pages = {s: bt[s, :(ln + 15) // 16].copy() for s, ln in lens.items()}
+    snap = {s: [(cache.k_cache[l][torch.from_numpy(p).long().to(gpu)].clone(),
+                 cache.v_cache[l][torch.from_numpy(p).long().to(gpu)].clone())
+                for l in range(layers)] for s, p in pages.items()}
+    ids = np.concatenate([pages[0], pages[2]])
+    ref = np.concatenate([orc.gather_blocks(u16(cache.k_cache[l]), u16(cache.v_cache[l]), ids)
+                          .ravel() for l in range(layers)])
+    h = cache.swap_out([0, 2])
+    cache.synchronize_swaps()
+    assert np.array_equal(h.host[:ref.size].numpy(), ref)
+    cache.fill_kv_random(1.0, generator=torch.Generator(device=gpu).manual_seed(82))
+    keep1 = [(cache.k_cache[l][torch.from_numpy(pages[1]).long().to(gpu)].clone())
+             for l in range(layers)]
+    cache.swap_in(h, seq_ids=[3, 0], wait=True)
+    torch.cuda.synchronize()
+    bt = cache.block_table.cpu().numpy()
+    for src, dst in ((0, 3), (2, 0)):
+        p = torch.from_numpy(bt[dst, :len(pages[src])]).long().to(gpu)
+        for l in range(layers):
+            assert torch.equal(cache.k_cache[l][p], snap[src][l][0])
+            assert torch.equal(cache.v_cache[l][p], snap[src][l][1])
+    for l in range(layers):
+        assert torch.equal(cache.k_cache[l][torch.from_numpy(pages[1]).long().to(gpu)], keep1[l])
+    assert [int(cache._seq_lens_cpu[s]) for s in (3, 0, 1, 2)] == [70, 64, 40, 0]
