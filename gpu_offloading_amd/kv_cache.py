@@ -184,23 +184,25 @@ class PagedKVCache:
         for j, p in enumerate(pages):
             self._bt_pending[base + j] = int(p)
 
-    def _take_bt_pending(self):
-        """(positions int64, values int32) of the pending writes, cleared."""
+    def _peek_bt_pending(self):
+        """(positions int64, values int32) of the pending writes, or None.
+        Callers clear ``_bt_pending`` once the writes are enqueued, so that an
+        error on the way leaves them pending."""
         if not self._bt_pending:
             return None
         pos = np.fromiter(self._bt_pending.keys(), dtype=np.int64, count=len(self._bt_pending))
         val = np.fromiter(self._bt_pending.values(), dtype=np.int32, count=len(self._bt_pending))
-        self._bt_pending.clear()
         return pos, val
 
     def _flush_block_table(self) -> None:
-        pend = self._take_bt_pending()
+        pend = self._peek_bt_pending()
         if pend is None:
             return
         pos, val = pend
         both = np.concatenate([pos, val.astype(np.int64)])
         d = self._to_device(both)
         self._bt.view(-1).scatter_(0, d[:len(pos)], d[len(pos):].to(torch.int32))
+        self._bt_pending.clear()
 
     def _require_gpu(self) -> None:
         if self._decode_wrapper is None:
@@ -443,7 +445,7 @@ class PagedKVCache:
         #   ids[b] | qsl[b+1] | lens_before[ms] | lens_after[ms] | kv_indptr[b+1]
         #   | last_page_len[b] | block-table positions (int64) | page ids
         #   | decode schedule (16-byte aligned)
-        pend = self._take_bt_pending()
+        pend = self._peek_bt_pending()
         u = 0 if pend is None else len(pend[0])
         w = self._decode_wrapper
         o_ids, o_qsl = 0, b
@@ -478,11 +480,11 @@ class PagedKVCache:
                 break
             cap = (sched.plan_ints + 3) // 4 * 4
         total = int(h[o_ip + b])
-        lens_all[ids] += 1
 
         dm = hs.to(self.device, non_blocking=True)
         if u:
             self._bt.view(-1).scatter_(0, dm[o_pos:o_val].view(torch.int64), dm[o_val:o_val + u])
+            self._bt_pending.clear()
         ids_d = dm[o_ids:o_qsl]
         slots = torch.empty(graph_n, dtype=torch.int64, device=self.device)
         ops.compute_slot_mapping(self._bt, ids_d, dm[o_qsl:o_lb], dm[o_lb:o_la], b, slots,
@@ -493,6 +495,7 @@ class PagedKVCache:
         w._install(sched, dm[o_plan:o_plan + cap], indptr_d, dm[o_lpl:o_lpl + b],
                    self._plan_indices_gpu[:total], self.num_heads, self.num_kv_heads,
                    self.head_dim, ps)
+        lens_all[ids] += 1
         return slots
 
     # ------------------------------------------------------- per-layer ops

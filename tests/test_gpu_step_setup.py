@@ -100,3 +100,33 @@ def test_block_table_reads_apply_pending_writes(gpu):
     assert cache._bt_pending
     assert np.array_equal(cache.block_table.cpu().numpy(), pool.block_table)
     assert not cache._bt_pending
+
+
+def test_failed_step_setup_leaves_state_untouched(gpu):
+    """A step whose plan fails (workspace too small for its split-K
+    partials) raises before anything is enqueued: pending block-table writes
+    stay pending, host lengths are not advanced, and the table still reads
+    back right."""
+    from gpu_offloading_amd.kv_cache import PagedKVCache
+
+    cache = PagedKVCache(1, 2, 128, max_seqs=2, max_seq_len=4096, num_qo_heads=8,
+                         kv_page_budget=500, free_page_order=workloads.randperm(500, 74),
+                         device=gpu, workspace_bytes=1024, staging_bytes=1 << 20)
+    pool = orc.FifoPagePool(500, 2, cache.max_pages_per_seq, free_order=workloads.randperm(500, 74))
+    for s, n in ((0, 4000), (1, 3000)):
+        cache.ensure_pages(s, (n + 1 + 15) // 16)
+        pool.ensure_pages(s, (n + 1 + 15) // 16)
+    cache.advance([0, 1], [4000, 3000])
+    _ = cache.block_table  # applies the writes so far
+    cache.free_seq(1)
+    pool.free_seq(1)
+    cache.ensure_pages(1, 3)
+    pool.ensure_pages(1, 3)
+    cache.advance([1], [40])
+    pending = dict(cache._bt_pending)
+    assert pending
+    with pytest.raises(RuntimeError, match="workspace"):
+        cache.prepare_decode_step([0, 1])
+    assert cache._bt_pending == pending
+    assert [int(x) for x in cache._seq_lens_cpu] == [4000, 40]
+    assert np.array_equal(cache.block_table.cpu().numpy(), pool.block_table)
