@@ -64,7 +64,6 @@ constexpr int kTokPerRow = 4;          // register kernel: tokens of a page per 
 constexpr int kIdRegs = 2;             // page-id registers per lane
 constexpr int kMaxSegPages = 64 * kIdRegs;
 constexpr int kReadGroup = 4;  // LDS reads scheduled together
-constexpr int kStages = 2;  // pages in flight per wave (LDS kernel)
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kLog2e = 1.44269504088896340736f;
 
