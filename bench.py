@@ -27,7 +27,8 @@ the same workload on the host cores.
 
 Other modes used by the profiles (one kernel family each, few launches):
   --mode copy     a plain device copy of known size (FETCH/WRITE calibration)
-  --mode decode2  configuration 2 decode, one layer, 10 launches
+  --mode decode2  configuration 2 decode with the fused 64-token append, one
+                  layer, 10 launches (--separate-append: decode alone)
   --mode decode4  configuration 4 decode only (32 launches)
   --mode append3  configuration 3 append + gather, one layer, 10 launches each
   --mode prefill3 continuation prefill after the cfg3 append (8 x 2048-token
@@ -82,6 +83,9 @@ def parse_args():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip configurations 3-5")
+    p.add_argument("--separate-append", action="store_true",
+                   help="append with reshape_and_cache_flash, then decode (two launches per "
+                        "layer) instead of the fused append_and_decode")
     p.add_argument("--mode", default="step",
                    choices=["step", "copy", "decode2", "decode4", "append3", "prefill3",
                             "xpacked", "offload"])
@@ -169,18 +173,25 @@ def run_step_bench(torch, args):
         dbytes = workloads.decode_bytes(lens_after, sh.num_qo_heads, sh.num_kv_heads, sh.head_dim)
         abytes = workloads.append_bytes(B, sh.num_kv_heads, sh.head_dim)
         for layer in range(L):
-            cache.append(layer, ks[layer], vs[layer], slots)
+            if args.separate_append:
+                cache.append(layer, ks[layer], vs[layer], slots)
+                run = lambda: cache.decode(layer, qs[layer], out=outs[layer])  # noqa: E731
+                lbytes = dbytes
+            else:
+                run = lambda: cache.append_and_decode(  # noqa: E731
+                    layer, ks[layer], vs[layer], qs[layer], out=outs[layer])
+                lbytes = dbytes + abytes
             # Events bracket every 8th layer's decode only: each recorded event
             # costs the stream a few microseconds.
             if timed["on"] and layer % 8 == 0:
                 e0, e1 = _events(torch)
                 e0.record()
-                cache.decode(layer, qs[layer], out=outs[layer])
+                run()
                 e1.record()
                 timed["pairs"].append((e0, e1))
-                timed["decode_bytes"].append(dbytes)
+                timed["decode_bytes"].append(lbytes)
             else:
-                cache.decode(layer, qs[layer], out=outs[layer])
+                run()
         if timed["on"]:
             timed["bytes"] += L * (dbytes + abytes)
 
@@ -211,7 +222,10 @@ def run_step_bench(torch, args):
         "value": step_gbps,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": profiled_traffic(),
-                     "kernel": "decode_lds_kernel<4, 8> + decode_merge_kernel<128>",
+                     "kernel": ("decode_lds_kernel<4, 8> + decode_merge_kernel<128>"
+                                + ("" if args.separate_append else
+                                   " (the step's 64-token append fused into the streaming "
+                                   "kernel: bytes per launch include it)")),
                      "avg_launch_us": avg_ms * 1e3, "algorithmic_bytes_per_launch": avg_bytes,
                      "segments": sched.num_segments, "head_groups": sched.num_head_groups,
                      "max_partitions": sched.max_partitions},
@@ -222,8 +236,10 @@ def run_step_bench(torch, args):
 
 
 # ----------------------------------------------------------- extras
-def run_decode2(torch, seed, reps=10):
-    """Configuration 2 decode attention (len + 1 tokens), one layer."""
+def run_decode2(torch, seed, reps=10, fused=True):
+    """Configuration 2 decode attention (len + 1 tokens), one layer; with
+    `fused` (the step's default) each launch also appends the step's 64 new
+    rows as the requests' last tokens (run_with_append)."""
     from gpu_offloading_amd import workloads
 
     cfg = workloads.config2(seed=seed)
@@ -232,16 +248,29 @@ def run_decode2(torch, seed, reps=10):
     kc, vc, q, w = build_paged(torch, lens, sh.num_kv_heads, sh.head_dim, seed + 3,
                                hq=sh.num_qo_heads)
     out = torch.empty_like(q)
-    w.run(q, (kc, vc), out=out)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 4)
+    nk = torch.randn(len(lens), sh.num_kv_heads, sh.head_dim, device="cuda",
+                     generator=g).to(torch.bfloat16)
+    nv = torch.randn_like(nk)
+    if fused:
+        def launch():
+            w.run_with_append(q, (kc, vc), nk, nv, out=out)
+    else:
+        def launch():
+            w.run(q, (kc, vc), out=out)
+    launch()
     torch.cuda.synchronize()
     e0, e1 = _events(torch)
     e0.record()
     for _ in range(reps):
-        w.run(q, (kc, vc), out=out)
+        launch()
     e1.record()
     torch.cuda.synchronize()
     t = e0.elapsed_time(e1) * 1e-3 / reps
     b = workloads.decode_bytes(lens, sh.num_qo_heads, sh.num_kv_heads, sh.head_dim)
+    if fused:
+        b += workloads.append_bytes(len(lens), sh.num_kv_heads, sh.head_dim)
     log(f"cfg2 decode: {t * 1e6:.1f} us, {b / t / 1e9:.0f} GB/s, {b} algorithmic bytes")
     print(json.dumps({"mode": "decode2", "us": t * 1e6, "bytes": b, "GBps": b / t / 1e9}),
           flush=True)
@@ -792,7 +821,7 @@ def main():
         run_copy_calibration(torch)
         return
     if args.mode == "decode2":
-        run_decode2(torch, args.seed)
+        run_decode2(torch, args.seed, fused=not args.separate_append)
         return
     if args.mode == "decode4":
         run_cfg4(torch, args.seed, decode_only=True)
@@ -837,7 +866,10 @@ def main():
                                "+ paged GQA decode), B=64, ctx U[512,4096], Hkv=8, Hq=32, D=128, "
                                "page 16, bf16; value = (decode + append algorithmic bytes) / step "
                                "wall time incl. host setup",
-                   "global_batch": 64, "layers": 32, "parallelism": "none (1 GPU)"},
+                   "global_batch": 64, "layers": 32, "parallelism": "none (1 GPU)",
+                   "append": ("separate reshape_and_cache_flash launch" if args.separate_append
+                              else "fused into the decode launch (append_and_decode; cache and "
+                                   "output bit-identical to the two calls)")},
         "roofline": res["roofline"],
         "cpu_baseline": cpu,
         "extra": extra,

@@ -51,6 +51,8 @@ class KvcDecodeSchedule(ctypes.Structure):
         ("heads_per_group", c_int32),
         ("plan_ints", c_int64),
         ("workspace_bytes", c_int64),
+        ("append_pieces", c_int32),
+        ("reserved", c_int32),
     ]
 
 
@@ -97,6 +99,10 @@ SIGNATURES = {
     "kvc_batch_decode_run": (c_int, [
         POINTER(KvcDecodeSchedule), _I32P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64,
         _I32P, _I32P, c_int64, _I32P, c_float, _P, c_int64, _P, c_int64, _P, _P]),
+    "kvc_batch_decode_append_run": (c_int, [
+        POINTER(KvcDecodeSchedule), _I32P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64,
+        _I32P, _I32P, c_int64, _I32P, _P, c_int64, _P, c_int64, c_float, _P, c_int64, _P,
+        c_int64, _P, _P]),
     "kvc_prefill_plan": (c_int, [
         c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
         POINTER(KvcPrefillSchedule), c_void_p, c_int64]),

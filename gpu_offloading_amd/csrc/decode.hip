@@ -94,7 +94,17 @@ struct DecodeArgs {
   uint16_t* out;
   int64_t out_stride;      // elements between requests
   float* lse;              // [batch][Hq] natural log, may be null
+  // Fused append (8 KV heads per workgroup): row b of new_k / new_v is
+  // written as request b's last token before it is attended; null: none.
+  const uint16_t* new_k;
+  const uint16_t* new_v;
+  int64_t new_k_stride;    // elements between requests
+  int64_t new_v_stride;
 };
+
+// Pieces, counted from a segment's first, within which a fused append's
+// request may end (the plan reports the most any segment needs).
+constexpr int kNewMax = 4;
 
 // Compiler-level ordering point for LDS traffic between lanes of one wave
 // (the LDS unit itself executes one wave's instructions in order).
@@ -234,6 +244,10 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
   constexpr int kSliceChunks = HPW * 16;  // 16-byte chunks per token row of the slice
   __shared__ Tile s_tile[2];
   __shared__ float s_p[HPW][kPage * 8];   // softmax weights p[token][query head]
+  // Fused append: the new rows (K, V) of the requests that end inside the
+  // segment, by piece index (8 heads per workgroup only).
+  constexpr bool kAppend = HPW == 8;
+  __shared__ uint4 s_new[kAppend ? kNewMax : 1][2][kAppend ? kSliceChunks : 1];
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -273,6 +287,30 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
   ids.load(a, g0, n, lane);
   Piece pc;
   pc.load(a, k);
+  const int k0 = k;
+  const bool appending = kAppend && a.new_k != nullptr;
+  // Thread i < 2 x kSliceChunks loads chunk i % kSliceChunks of the K (or V)
+  // slice of each new row; the rows land in s_new after the first pages'
+  // loads are issued.
+  // The loads are issued on every path (a piece past the segment's last
+  // re-reads that one's row), so the compiler's count of loads in flight stays
+  // exact and staging s_new does not wait for the first pages' loads.
+  uint4 nrow[kAppend ? kNewMax : 1];
+#pragma unroll
+  for (int i = 0; i < (kAppend ? kNewMax : 1); ++i) nrow[i] = make_uint4(0, 0, 0, 0);
+  if constexpr (kAppend) {
+    if (appending) {
+      const int is_v = (threadIdx.x & (2 * kSliceChunks - 1)) >= kSliceChunks;
+      const int cc = threadIdx.x & (kSliceChunks - 1);
+#pragma unroll
+      for (int i = 0; i < kNewMax; ++i) {
+        const int b = a.pieces[2 * min(k + i, k_end - 1)].x;
+        const uint16_t* src = is_v ? a.new_v + int64_t(b) * a.new_v_stride
+                                   : a.new_k + int64_t(b) * a.new_k_stride;
+        nrow[i] = reinterpret_cast<const uint4*>(src + h0 * D)[cc];
+      }
+    }
+  }
 
   uint32_t qw[C::QL][C::CH * 4];
   auto load_q = [&](int b) __attribute__((always_inline)) {
@@ -424,6 +462,26 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
   auto step = [&](int j, Stage& r, int32_t& id, Tile& tile) __attribute__((always_inline)) {
     const int slot = g0 + j;
     const int valid = pc.valid(slot, id, a.num_blocks);
+    if constexpr (kAppend) {
+      // The request's last page: its new token row comes from s_new (the
+      // loaded row is stale) and is written to the cache.
+      if (appending && slot == pc.req_last && valid > 0 && k - k0 < kNewMax) {
+        const int tnew = valid - 1;
+        const int i = k - k0;
+        char* kdst = const_cast<char*>(kbytes) + int64_t(id) * block_bytes;
+        char* vdst = const_cast<char*>(vbytes) + int64_t(id) * block_bytes;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (st_tok[u] == tnew) {
+            const int cc = st_loff[u] - st_tok[u] * Tile::kRowChunks;
+            r.k[u] = s_new[i][0][cc];
+            r.v[u] = s_new[i][1][cc];
+            store_stream(kdst + st_goff[u], r.k[u]);
+            store_stream(vdst + st_goff[u], r.v[u]);
+          }
+        }
+      }
+    }
     stage_tile(r, tile, valid);
     if (j + 2 < n) {
       id = ids.at(j + 2);
@@ -450,6 +508,17 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
   if (n > 1) {
     idb = ids.at(1);
     issue(rb, safe_id(idb));
+  }
+  if constexpr (kAppend) {
+    if (appending) {
+      if (threadIdx.x < 2 * kSliceChunks) {
+        const int is_v = threadIdx.x >= kSliceChunks;
+        const int cc = threadIdx.x & (kSliceChunks - 1);
+#pragma unroll
+        for (int i = 0; i < kNewMax; ++i) s_new[i][is_v][cc] = nrow[i];
+      }
+      __syncthreads();
+    }
   }
   for (int j = 0; j < n; j += 2) {
     step(j, ra, ida, s_tile[0]);
@@ -932,6 +1001,7 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, const int32_t* last_p
   std::fill(nparts, nparts + batch, 0);
   int64_t np = 0;
   int b = 0;
+  int32_t append_pieces = 0;
   for (int64_t s = 0; s < segs; ++s) {
     const int64_t g0 = s * total / segs;
     const int64_t g1 = (s + 1) * total / segs;
@@ -953,6 +1023,10 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, const int32_t* last_p
         pc[5] = last_page_len_host ? last_page_len_host[bb] : kPage;
         pc[6] = 0;
         pc[7] = 0;
+        // a request ending here: the fused append stages its new row by the
+        // piece's index within the segment
+        if (se == indptr_host[bb + 1])
+          append_pieces = std::max<int32_t>(append_pieces, int32_t(np - rec[0]));
       }
     }
     rec[1] = int32_t(np);
@@ -968,17 +1042,20 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, const int32_t* last_p
   sched->max_partitions = max_parts;
   sched->workspace_bytes =
       kvc_decode_workspace_bytes(batch, num_qo_heads, head_dim, max_parts);
+  sched->append_pieces = append_pieces;
+  sched->reserved = 0;
   return ok();
 }
 
-extern "C" int kvc_batch_decode_run(
-    const kvc_decode_schedule* sched, const int32_t* plan, const void* q,
-    int64_t q_batch_stride, const void* key_cache, const void* value_cache,
-    int64_t cache_block_stride, int64_t cache_token_stride, int64_t num_blocks,
-    const int32_t* indptr, const int32_t* indices, int64_t num_indices,
-    const int32_t* last_page_len, float sm_scale, void* workspace,
-    int64_t workspace_bytes, void* out, int64_t out_batch_stride, float* lse,
-    void* stream) {
+namespace {
+int decode_run(const kvc_decode_schedule* sched, const int32_t* plan, const void* q,
+               int64_t q_batch_stride, const void* key_cache, const void* value_cache,
+               int64_t cache_block_stride, int64_t cache_token_stride, int64_t num_blocks,
+               const int32_t* indptr, const int32_t* indices, int64_t num_indices,
+               const int32_t* last_page_len, const void* new_key, int64_t new_key_stride,
+               const void* new_value, int64_t new_value_stride, float sm_scale,
+               void* workspace, int64_t workspace_bytes, void* out, int64_t out_batch_stride,
+               float* lse, void* stream) {
   KVC_REQUIRE(sched, KVC_ERR_INVALID_ARG, "null schedule");
   const int batch = sched->batch;
   if (batch == 0) return ok();
@@ -1046,6 +1123,23 @@ extern "C" int kvc_batch_decode_run(
   a.out = static_cast<uint16_t*>(out);
   a.out_stride = out_batch_stride;
   a.lse = lse;
+  a.new_k = static_cast<const uint16_t*>(new_key);
+  a.new_v = static_cast<const uint16_t*>(new_value);
+  a.new_k_stride = new_key_stride;
+  a.new_v_stride = new_value_stride;
+  if (new_key || new_value) {
+    KVC_REQUIRE(new_key && new_value, KVC_ERR_INVALID_ARG, "new_key and new_value go together");
+    KVC_REQUIRE(D == 128 && sched->heads_per_group == 8 && sched->append_pieces <= kNewMax,
+                KVC_ERR_UNSUPPORTED,
+                "fused append needs head_dim 128, a multiple of 8 KV heads with group <= 4, "
+                "and at most " + std::to_string(kNewMax) + " leading pieces per segment "
+                "holding request ends (schedule->append_pieces)");
+    KVC_REQUIRE(new_key_stride >= int64_t(Hkv) * D && new_value_stride >= int64_t(Hkv) * D,
+                KVC_ERR_INVALID_ARG, "new row stride smaller than a row");
+    KVC_REQUIRE(aligned(new_key, 16) && aligned(new_value, 16) && new_key_stride % 8 == 0 &&
+                    new_value_stride % 8 == 0,
+                KVC_ERR_ALIGNMENT, "new rows must be 16-byte aligned");
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   if (sched->num_segments > 0) {
@@ -1080,6 +1174,38 @@ extern "C" int kvc_batch_decode_run(
   else decode_merge_kernel<256><<<mgrid, 64, 0, s>>>(m);
   KVC_LAUNCH_CHECK();
   return ok();
+}
+
+}  // namespace
+
+extern "C" int kvc_batch_decode_run(
+    const kvc_decode_schedule* sched, const int32_t* plan, const void* q,
+    int64_t q_batch_stride, const void* key_cache, const void* value_cache,
+    int64_t cache_block_stride, int64_t cache_token_stride, int64_t num_blocks,
+    const int32_t* indptr, const int32_t* indices, int64_t num_indices,
+    const int32_t* last_page_len, float sm_scale, void* workspace,
+    int64_t workspace_bytes, void* out, int64_t out_batch_stride, float* lse,
+    void* stream) {
+  return decode_run(sched, plan, q, q_batch_stride, key_cache, value_cache, cache_block_stride,
+                    cache_token_stride, num_blocks, indptr, indices, num_indices, last_page_len,
+                    nullptr, 0, nullptr, 0, sm_scale, workspace, workspace_bytes, out,
+                    out_batch_stride, lse, stream);
+}
+
+extern "C" int kvc_batch_decode_append_run(
+    const kvc_decode_schedule* sched, const int32_t* plan, const void* q,
+    int64_t q_batch_stride, const void* key_cache, const void* value_cache,
+    int64_t cache_block_stride, int64_t cache_token_stride, int64_t num_blocks,
+    const int32_t* indptr, const int32_t* indices, int64_t num_indices,
+    const int32_t* last_page_len, const void* new_key, int64_t new_key_stride,
+    const void* new_value, int64_t new_value_stride, float sm_scale, void* workspace,
+    int64_t workspace_bytes, void* out, int64_t out_batch_stride, float* lse,
+    void* stream) {
+  KVC_REQUIRE(new_key && new_value, KVC_ERR_INVALID_ARG, "null new_key or new_value");
+  return decode_run(sched, plan, q, q_batch_stride, key_cache, value_cache, cache_block_stride,
+                    cache_token_stride, num_blocks, indptr, indices, num_indices, last_page_len,
+                    new_key, new_key_stride, new_value, new_value_stride, sm_scale, workspace,
+                    workspace_bytes, out, out_batch_stride, lse, stream);
 }
 
 extern "C" int kvc_merge_attention_states(const void* out1, const float* lse1,

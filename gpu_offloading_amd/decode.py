@@ -234,10 +234,68 @@ class BatchDecodeWithPagedKVCacheWrapper:
         (bf16 ``[B, num_qo_heads, head_dim]``) or ``(out, lse)``; lse is the
         natural-log log-sum-exp of the scaled logits.
         """
-        if self._sched is None:
-            _fail("run() called before plan()")
         if any(s not in (None, 1.0) for s in (q_scale, k_scale, v_scale)):
             _fail("q/k/v scales are not supported (bf16 cache)")
+        k_cache, v_cache, out, lse = self._run_args(q, paged_kv_cache, out, lse, return_lse)
+        s = stream if stream is not None else torch.cuda.current_stream(self._device)
+        ws = self._workspace
+        _lib.call("kvc_batch_decode_run", self._sched, self._plan_dev.data_ptr(),
+                  q.data_ptr(), q.stride(0),
+                  k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
+                  k_cache.shape[0], self._indptr.data_ptr(), self._indices.data_ptr(),
+                  self._num_indices, self._lpl.data_ptr(), self._sm_scale, ws.data_ptr(),
+                  ws.numel() * ws.element_size(), out.data_ptr(), out.stride(0),
+                  lse.data_ptr() if lse is not None else None, s.cuda_stream)
+        return (out, lse) if return_lse else out
+
+    forward = run
+
+    @property
+    def fused_append_supported(self) -> bool:
+        """Whether ``run_with_append`` can serve the planned batch (head_dim
+        128, 8 KV heads per workgroup, few request ends per segment)."""
+        sc = self._sched
+        return (sc is not None and sc.head_dim == 128 and sc.heads_per_group == 8
+                and sc.append_pieces <= 4)
+
+    def run_with_append(self, q: torch.Tensor,
+                        paged_kv_cache: Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]],
+                        new_key: torch.Tensor, new_value: torch.Tensor, *,
+                        out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
+                        return_lse: bool = False, stream: Optional[torch.cuda.Stream] = None):
+        """``run`` that first writes ``new_key[b]`` / ``new_value[b]``
+        (``[B, num_kv_heads, head_dim]`` bf16) into the cache as request b's
+        last token -- the slot a pure-decode step's slot mapping gives it --
+        in the same launch (``kvc_batch_decode_append_run``).  Cache and
+        output equal ``reshape_and_cache_flash`` followed by ``run`` bit for
+        bit.  Raises unless ``fused_append_supported``."""
+        if not self.fused_append_supported:
+            _fail("the fused append needs head_dim 128, num_kv_heads a multiple of 8, "
+                  "group <= 4 and at most 4 request ends in a segment's leading pieces")
+        k_cache, v_cache, out, lse = self._run_args(q, paged_kv_cache, out, lse, return_lse)
+        batch, hq, hkv, d, ps = self._plan_args
+        for name, t in (("new_key", new_key), ("new_value", new_value)):
+            if (t.dtype != torch.bfloat16 or t.dim() != 3 or t.shape[0] < batch
+                    or tuple(t.shape[1:]) != (hkv, d) or t.stride(2) != 1 or t.stride(1) != d):
+                _fail(f"{name} must be bfloat16 [B, {hkv}, {d}] with contiguous heads")
+            if t.device != self._device:
+                _fail(f"{name} on a different device than the workspace")
+        s = stream if stream is not None else torch.cuda.current_stream(self._device)
+        ws = self._workspace
+        _lib.call("kvc_batch_decode_append_run", self._sched, self._plan_dev.data_ptr(),
+                  q.data_ptr(), q.stride(0),
+                  k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
+                  k_cache.shape[0], self._indptr.data_ptr(), self._indices.data_ptr(),
+                  self._num_indices, self._lpl.data_ptr(), new_key.data_ptr(), new_key.stride(0),
+                  new_value.data_ptr(), new_value.stride(0), self._sm_scale, ws.data_ptr(),
+                  ws.numel() * ws.element_size(), out.data_ptr(), out.stride(0),
+                  lse.data_ptr() if lse is not None else None, s.cuda_stream)
+        return (out, lse) if return_lse else out
+
+    def _run_args(self, q, paged_kv_cache, out, lse, return_lse):
+        """Check run()'s tensors against the plan; allocate out / lse."""
+        if self._sched is None:
+            _fail("run() called before plan()")
         batch, hq, hkv, d, ps = self._plan_args
         if isinstance(paged_kv_cache, (tuple, list)):
             k_cache, v_cache = paged_kv_cache
@@ -272,18 +330,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
         if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()
                                 or lse.numel() < batch * hq):
             _fail("lse must be contiguous float32 [B, num_qo_heads]")
-        s = stream if stream is not None else torch.cuda.current_stream(self._device)
-        ws = self._workspace
-        _lib.call("kvc_batch_decode_run", self._sched, self._plan_dev.data_ptr(),
-                  q.data_ptr(), q.stride(0),
-                  k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
-                  k_cache.shape[0], self._indptr.data_ptr(), self._indices.data_ptr(),
-                  self._num_indices, self._lpl.data_ptr(), self._sm_scale, ws.data_ptr(),
-                  ws.numel() * ws.element_size(), out.data_ptr(), out.stride(0),
-                  lse.data_ptr() if lse is not None else None, s.cuda_stream)
-        return (out, lse) if return_lse else out
-
-    forward = run
+        return k_cache, v_cache, out, lse
 
     def end_forward(self) -> None:
         """No-op kept for interface parity."""

@@ -115,6 +115,8 @@ class PagedKVCache:
         # id, last write wins) until the next decode step uploads them with
         # the rest of its metadata, or ``block_table`` is read.
         self._bt_pending: dict[int, int] = {}
+        # slots of the step set up by prepare_decode_step (append_and_decode)
+        self._step_slots: Optional[torch.Tensor] = None
         self.seq_lens = torch.zeros(max_seqs, dtype=torch.int32, device=self.device)
         self._seq_lens_cpu = torch.zeros(max_seqs, dtype=torch.int32)
         self._pool = PagePool(self.total_pages, max_seqs, self.max_pages_per_seq,
@@ -273,6 +275,7 @@ class PagedKVCache:
     def reset(self) -> None:
         """moe_engine.py:4185-4210: zero lengths and caches, refill the pool."""
         self.synchronize_swaps()
+        self._step_slots = None
         self.seq_lens.zero_()
         self._seq_lens_cpu.zero_()
         for kc, vc in zip(self.k_cache, self.v_cache):
@@ -349,6 +352,7 @@ class PagedKVCache:
         """moe_engine.py:1896-1955: indptr / last_page_len on the host,
         page indices flattened on the device, then ``wrapper.plan``."""
         self._require_gpu()
+        self._step_slots = None
         b = len(seq_ids)
         if b == 0:
             return
@@ -375,6 +379,7 @@ class PagedKVCache:
         (query rows are the last ``chunk_lens[i]`` tokens of each sequence,
         causal against everything cached)."""
         self._require_gpu()
+        self._step_slots = None
         b = len(seq_ids)
         if len(chunk_lens) != b:
             raise ValueError("one chunk length per sequence")
@@ -429,6 +434,7 @@ class PagedKVCache:
         self._require_gpu()
         b = len(seq_ids)
         graph_n = b if graph_n is None else graph_n
+        self._step_slots = None
         if b == 0 or graph_n < b:
             # Nothing to plan, or an error for slot_mapping to report.
             slots = self.slot_mapping(seq_ids, [1] * b, graph_n)
@@ -496,6 +502,7 @@ class PagedKVCache:
                    self._plan_indices_gpu[:total], self.num_heads, self.num_kv_heads,
                    self.head_dim, ps)
         lens_all[ids] += 1
+        self._step_slots = slots[:b]
         return slots
 
     # ------------------------------------------------------- per-layer ops
@@ -503,6 +510,26 @@ class PagedKVCache:
                slot_mapping: torch.Tensor) -> None:
         ops.reshape_and_cache_flash(key, value, self.k_cache[layer], self.v_cache[layer],
                                     slot_mapping, "auto")
+
+    def append_and_decode(self, layer: int, key: torch.Tensor, value: torch.Tensor,
+                          q: torch.Tensor, out: Optional[torch.Tensor] = None,
+                          return_lse: bool = False):
+        """``append(layer, key, value, slots)`` then ``decode(layer, q)`` for
+        the step set up by the last ``prepare_decode_step``: one launch when
+        the decode wrapper supports the fused append, else the two calls.
+        ``key``/``value`` are the step's new rows ``[B, Hkv, D]`` in the order
+        of that call's ``seq_ids``; the result is the same either way, bit for
+        bit."""
+        self._require_gpu()
+        slots = self._step_slots
+        if slots is None:
+            raise RuntimeError("append_and_decode needs a prepare_decode_step first")
+        w = self._decode_wrapper
+        if w.fused_append_supported:
+            return w.run_with_append(q, (self.k_cache[layer], self.v_cache[layer]), key, value,
+                                     out=out, return_lse=return_lse)
+        self.append(layer, key, value, slots)
+        return self.decode(layer, q, out=out, return_lse=return_lse)
 
     def decode(self, layer: int, q: torch.Tensor, out: Optional[torch.Tensor] = None,
                return_lse: bool = False):

@@ -138,6 +138,9 @@ typedef struct kvc_decode_schedule {
   int32_t heads_per_group;  /* KV heads one workgroup streams together     */
   int64_t plan_ints;        /* int32 entries of the plan image             */
   int64_t workspace_bytes;  /* bytes kvc_batch_decode_run will use         */
+  int32_t append_pieces;    /* most leading pieces of a segment that reach
+                               a request end (fused append supports <= 4)  */
+  int32_t reserved;
 } kvc_decode_schedule;
 
 int64_t kvc_decode_plan_ints(int32_t batch, int32_t num_segments);
@@ -164,6 +167,30 @@ int kvc_batch_decode_run(
     float sm_scale,
     void* workspace, int64_t workspace_bytes,
     void* out, int64_t out_batch_stride, float* lse, void* stream);
+
+/* Fused append + decode for a pure-decode step.  No single counterpart in
+ * the reference: it does, in one launch, what the engine does with
+ * reshape_and_cache_flash of the step's tokens (moe_engine.py:2344-2347)
+ * followed by the decode run (:3907-3909).  Row b of new_key / new_value
+ * ([batch][num_kv_heads][head_dim], new_*_stride elements between rows) is
+ * written to the cache as request b's last token -- page
+ * indices[indptr[b+1]-1], offset last_page_len[b]-1, i.e. the slot the step's
+ * slot mapping gives it -- and attended with the rest of the request.
+ * Requests with no pages append nothing.  The cache and the output equal
+ * those of the two separate calls bit for bit.  Needs head_dim 128, a
+ * multiple of 8 KV heads, group <= 4 and schedule->append_pieces <= 4;
+ * otherwise KVC_ERR_UNSUPPORTED (the caller then makes the two calls). */
+int kvc_batch_decode_append_run(
+    const kvc_decode_schedule* schedule, const int32_t* plan,
+    const void* q, int64_t q_batch_stride,
+    const void* key_cache, const void* value_cache,
+    int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t num_blocks, const int32_t* indptr, const int32_t* indices,
+    int64_t num_indices, const int32_t* last_page_len,
+    const void* new_key, int64_t new_key_stride,
+    const void* new_value, int64_t new_value_stride, float sm_scale,
+    void* workspace, int64_t workspace_bytes, void* out,
+    int64_t out_batch_stride, float* lse, void* stream);
 
 /* ------------------------------------------------------------------------
  * (f2) Paged-KV prefill attention: multi-token queries over the paged cache
