@@ -183,7 +183,7 @@ int kvc_batch_decode_run(
 int kvc_batch_decode_append_run(
     const kvc_decode_schedule* schedule, const int32_t* plan,
     const void* q, int64_t q_batch_stride,
-    const void* key_cache, const void* value_cache,
+    void* key_cache, void* value_cache,
     int64_t cache_block_stride, int64_t cache_token_stride,
     int64_t num_blocks, const int32_t* indptr, const int32_t* indices,
     int64_t num_indices, const int32_t* last_page_len,
