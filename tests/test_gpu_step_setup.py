@@ -130,3 +130,32 @@ def test_failed_step_setup_leaves_state_untouched(gpu):
     assert cache._bt_pending == pending
     assert [int(x) for x in cache._seq_lens_cpu] == [4000, 40]
     assert np.array_equal(cache.block_table.cpu().numpy(), pool.block_table)
+
+
+def test_static_pages_step(gpu):
+    """Static mode (identity block table, no allocator): the one-copy step
+    setup and the fused append + decode over the identity pages."""
+    from gpu_offloading_amd.kv_cache import PagedKVCache
+
+    lens = [5, 16, 40]
+    cache = PagedKVCache(1, 8, 128, max_seqs=3, max_seq_len=64, num_qo_heads=32, device=gpu,
+                         workspace_bytes=1 << 22, staging_bytes=1 << 20)
+    g = torch.Generator(device=gpu).manual_seed(75)
+    cache.fill_kv_random(1.0, generator=g)
+    cache.advance([0, 1, 2], lens)
+    slots = cache.prepare_decode_step([2, 0, 1], graph_n=4)
+    bt = np.arange(3 * 4, dtype=np.int32).reshape(3, 4)
+    exp, _ = orc.step_slot_mapping(bt, [2, 0, 1], [1, 1, 1], np.array(lens), 4)
+    assert np.array_equal(slots.cpu().numpy(), exp)
+    k = torch.randn(3, 8, 128, generator=g, device=gpu).to(torch.bfloat16)
+    v = torch.randn(3, 8, 128, generator=g, device=gpu).to(torch.bfloat16)
+    q = torch.randn(3, 32, 128, generator=g, device=gpu).to(torch.bfloat16)
+    out = cache.append_and_decode(0, k, v, q)
+    torch.cuda.synchronize()
+    new = [lens[s] + 1 for s in (2, 0, 1)]
+    indptr, lpl = orc.plan_decode(new)
+    idx = orc.page_indices(bt, [2, 0, 1], indptr)
+    ref, _ = orc.paged_decode(u16(q), u16(cache.k_cache[0]), u16(cache.v_cache[0]), indptr, idx, lpl)
+    assert_attn_close(out.float().cpu().numpy(), ref)
+    flat = u16(cache.k_cache[0]).reshape(-1, 8, 128)
+    assert np.array_equal(flat[exp[:3]], u16(k))
