@@ -342,7 +342,8 @@ def run_cfg3(torch, seed, reps=10, layers=None):
 
 def build_paged(torch, lens, hkv, d, seed, q_std=1.0, hq=32):
     """Device caches holding sequences `lens` in a seeded permuted pool, plus
-    a planned decode wrapper."""
+    a planned decode wrapper.  K and V are views of one [pages, 2, 16, Hkv, D]
+    tensor, the layout PagedKVCache allocates."""
     from gpu_offloading_amd import workloads
     from gpu_offloading_amd.decode import BatchDecodeWithPagedKVCacheWrapper
     import numpy as np
@@ -357,8 +358,8 @@ def build_paged(torch, lens, hkv, d, seed, q_std=1.0, hq=32):
     lpl = np.array([ln % 16 or 16 for ln in lens], np.int32)
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
-    kc = torch.empty(total, 16, hkv, d, dtype=torch.bfloat16, device="cuda")
-    vc = torch.empty_like(kc)
+    kv = torch.empty(total, 2, 16, hkv, d, dtype=torch.bfloat16, device="cuda")
+    kc, vc = kv[:, 0], kv[:, 1]
     kc.normal_(0, 1, generator=g)
     vc.normal_(0, 1, generator=g)
     q = (torch.randn(len(lens), hq, d, device="cuda", generator=g) * q_std).to(torch.bfloat16)
