@@ -295,8 +295,11 @@ def run_cfg3(torch, seed, reps=10, layers=None):
     bt = bt.cuda()
     n = slots.numel()
     shape = (cfg.total_pages, 16, sh.num_kv_heads, sh.head_dim)
-    kcs = [torch.zeros(shape, dtype=torch.bfloat16, device="cuda") for _ in range(L)]
-    vcs = [torch.zeros(shape, dtype=torch.bfloat16, device="cuda") for _ in range(L)]
+    # the PagedKVCache layout: K and V of a page adjacent, one tensor per layer
+    kvs = [torch.zeros((shape[0], 2) + tuple(shape[1:]), dtype=torch.bfloat16, device="cuda")
+           for _ in range(L)]
+    kcs = [t[:, 0] for t in kvs]
+    vcs = [t[:, 1] for t in kvs]
     k = [torch.randn(n, sh.num_kv_heads, sh.head_dim, device="cuda").to(torch.bfloat16) for _ in range(2)]
     v = [torch.randn(n, sh.num_kv_heads, sh.head_dim, device="cuda").to(torch.bfloat16) for _ in range(2)]
     ok = torch.empty(n, sh.num_kv_heads, sh.head_dim, dtype=torch.bfloat16, device="cuda")
