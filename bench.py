@@ -744,10 +744,11 @@ def run_cfg5(torch, seed, decode_steps=6):
 
 
 # ----------------------------------------------------------- CPU baseline
-def run_cpu_baseline(seed, reps=3):
+def run_cpu_baseline(seed, target_s=10.0, min_reps=3):
     """The numpy oracle (the CPU restatement of the reference path) on one
     layer of configuration 2: append of the 64 new tokens, then fp32 decode
-    attention over len + 1 tokens of all 64 sequences; single-threaded."""
+    attention over len + 1 tokens of all 64 sequences; single-threaded,
+    repeated for about `target_s` seconds of CPU work."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
@@ -779,9 +780,11 @@ def run_cpu_baseline(seed, reps=3):
               + workloads.append_bytes(B, sh.num_kv_heads, sh.head_dim))
     with threadpool_limits(limits=1):
         t0 = time.perf_counter()
-        for _ in range(reps):
+        reps = 0
+        while reps < min_reps or time.perf_counter() - t0 < target_s:
             orc.reshape_and_cache(kn, vn, kc, vc, slots)
             orc.paged_decode(q, kc, vc, indptr, indices, lpl)
+            reps += 1
         dt = time.perf_counter() - t0
     gbps = nbytes * reps / dt / 1e9
     log(f"cpu baseline: {gbps:.3f} GB/s over {dt:.1f} s")
