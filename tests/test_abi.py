@@ -116,6 +116,14 @@ def _check_plan_image(indptr, sched, img, lpl):
         else:
             assert mine[:, 3].tolist() == list(range(len(mine)))
     assert sched.max_partitions == max(1, int(nparts.max()))
+    # append_pieces: over segments, the most leading pieces up to the last
+    # one that ends its request (the fused append stages rows by this index)
+    want = 0
+    for s in range(S):
+        ps = rec[segs[s, 0]:segs[s, 1]]
+        ends = [i + 1 for i, pc in enumerate(ps) if pc[2] == pc[4] + 1]
+        want = max([want] + ends)
+    assert sched.append_pieces == want
 
 
 def test_decode_plan_is_host_only_and_balanced(lib):
@@ -132,6 +140,11 @@ def test_decode_plan_is_host_only_and_balanced(lib):
     indptr, sched, img, lpl = _plan(lib, [3000] * 64)
     assert sched.num_segments == 256
     _check_plan_image(indptr, sched, img, lpl)
+    assert sched.append_pieces == 1          # a segment holds at most one request end
+    # many short requests: several ends per segment (the fused append falls back)
+    indptr, sched, img, lpl = _plan(lib, [3] * 1500)
+    _check_plan_image(indptr, sched, img, lpl)
+    assert sched.append_pieces > 4
     # KV heads that do not divide by 8 stream one per workgroup
     indptr, sched, img, lpl = _plan(lib, [3000] * 64, hq=24, hkv=6)
     assert sched.heads_per_group == 1 and sched.num_head_groups == 6
