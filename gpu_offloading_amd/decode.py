@@ -49,6 +49,13 @@ class BatchDecodeWithPagedKVCacheWrapper:
                  num_segments: Optional[int] = None):
         if kv_layout != "NHD":
             _fail(f"kv_layout={kv_layout!r} is not supported (only 'NHD')")
+        if use_cuda_graph:
+            # FlashInfer's graph mode re-plans into fixed buffers between
+            # replays; here plan() stages a new schedule image per call (a
+            # captured run() stays valid only until the next plan()).  The
+            # engine constructs its wrapper with use_cuda_graph=False
+            # (moe_engine.py:551-552).
+            _fail("use_cuda_graph=True is not supported (capture run() within one plan instead)")
         if not float_workspace_buffer.is_cuda:
             _fail("float_workspace_buffer must be a GPU tensor")
         self._workspace = float_workspace_buffer

@@ -51,6 +51,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
                  use_cuda_graph: bool = False, **kwargs):
         if kv_layout != "NHD":
             _fail(f"kv_layout={kv_layout!r} is not supported (only 'NHD')")
+        if use_cuda_graph:
+            _fail("use_cuda_graph=True is not supported (capture run() within one plan instead)")
         if not float_workspace_buffer.is_cuda:
             _fail("float_workspace_buffer must be a GPU tensor")
         self._device = float_workspace_buffer.device
