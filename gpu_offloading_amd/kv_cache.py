@@ -449,10 +449,18 @@ class PagedKVCache:
         self._sync_seqs(seq_ids)
         ids = np.asarray(seq_ids, dtype=np.int64)
         lens_all = self._seq_lens_cpu.numpy()
-        if len(np.unique(ids)) != b:
-            raise ValueError("seq_ids must be distinct")
         ms, ps = self.max_seqs, self.page_size
+        if ids.min() < 0 or ids.max() >= ms or len(np.unique(ids)) != b:
+            raise ValueError(f"seq_ids must be distinct and in [0, {ms})")
         lens = lens_all[ids].astype(np.int32) + 1
+        if int(lens.max()) > self.max_pages_per_seq * ps:
+            raise RuntimeError(f"a sequence would exceed max_seq_len ({self.max_pages_per_seq * ps})")
+        if self._dynamic_pages:
+            short = [int(s) for s, n in zip(ids, lens)
+                     if self._pool.seq_pages(int(s)) * ps < n]
+            if short:
+                raise RuntimeError(f"sequences {short} have no page for the new token "
+                                   "(ensure_pages first)")
 
         # One pinned int32 image of the step's metadata, one H2D copy:
         #   ids[b] | qsl[b+1] | lens_before[ms] | lens_after[ms] | kv_indptr[b+1]

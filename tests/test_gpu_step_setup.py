@@ -159,3 +159,24 @@ def test_static_pages_step(gpu):
     assert_attn_close(out.float().cpu().numpy(), ref)
     flat = u16(cache.k_cache[0]).reshape(-1, 8, 128)
     assert np.array_equal(flat[exp[:3]], u16(k))
+
+
+def test_step_setup_rejects_bad_requests(gpu):
+    from gpu_offloading_amd.kv_cache import PagedKVCache
+
+    cache = PagedKVCache(1, 8, 128, max_seqs=3, max_seq_len=32, num_qo_heads=32,
+                         kv_page_budget=8, device=gpu, workspace_bytes=1 << 20,
+                         staging_bytes=1 << 20)
+    cache.ensure_pages(0, 1)
+    cache.advance([0], [16])                  # page 0 full: the next token needs page 1
+    with pytest.raises(RuntimeError, match="ensure_pages"):
+        cache.prepare_decode_step([0])
+    with pytest.raises(ValueError, match="distinct"):
+        cache.prepare_decode_step([1, 1])
+    with pytest.raises(ValueError, match="distinct"):
+        cache.prepare_decode_step([-1])
+    cache.ensure_pages(0, 2)
+    cache.advance([0], [16])                  # 32 tokens: max_seq_len reached
+    with pytest.raises(RuntimeError, match="max_seq_len"):
+        cache.prepare_decode_step([0])
+    assert [int(x) for x in cache._seq_lens_cpu] == [32, 0, 0]
