@@ -38,6 +38,8 @@ Other modes used by the profiles (one kernel family each, few launches):
                   reshape_and_cache, 10 launches each
   --mode offload  layer-wise KV offload pipeline (8 layers, 25% of blocks in
                   host memory) and swap preemption of a 4096-token request
+  --mode swap5    configuration 5 swap out / swap in of 32 of 128 sequences
+                  (16 layers) while the other 96 decode
 """
 from __future__ import annotations
 
@@ -88,7 +90,7 @@ def parse_args():
                         "layer) instead of the fused append_and_decode")
     p.add_argument("--mode", default="step",
                    choices=["step", "copy", "decode2", "decode4", "append3", "prefill3",
-                            "xpacked", "offload"])
+                            "xpacked", "offload", "swap5"])
     return p.parse_args()
 
 
@@ -671,8 +673,9 @@ def run_cfg5(torch, seed, decode_steps=6):
                     generator=g).to(torch.bfloat16)
     out = torch.empty_like(q)
 
+    cache.plan_decode(running)   # the running set and its lengths stay fixed
+
     def decode_pass():
-        cache.plan_decode(running)
         for layer in range(L):
             cache.decode(layer, q, out=out)
 
@@ -693,34 +696,46 @@ def run_cfg5(torch, seed, decode_steps=6):
     bb = 2 * cache.k_cache[0][0].numel() * cache.k_cache[0].element_size()
     npages = sum(cache.seq_pages(s) for s in victims)
     host = torch.empty(L * npages * bb, dtype=torch.uint8, pin_memory=True)
+    nbytes_est = L * npages * bb
 
-    # swap out under load: decode steps of the running sequences keep being
-    # issued on the current stream until the side stream has finished
-    h = cache.swap_out(victims, host=host)
-    e0.record()
-    n_dec = 0
-    while not h.out_event.query():
-        decode_pass()
-        n_dec += 1
-        torch.cuda.current_stream().synchronize()
-    e1.record()
-    h.out_event.synchronize()
-    torch.cuda.synchronize()
+    def under_swap(start_swap):
+        """Start a swap, then enqueue decode passes back to back on the
+        current stream (no host waits) for about 1.5x the swap's expected
+        time at 50 GB/s; the mean GPU time of the passes that ran entirely
+        between the swap's start and end events is the decode time under
+        load."""
+        n_pass = max(8, int(1.5 * nbytes_est / 50e9 / t_alone))
+        t0 = time.perf_counter()
+        h_, ev_start, ev_end = start_swap()
+        host_ms = (time.perf_counter() - t0) * 1e3
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(n_pass + 1)]
+        marks[0].record()
+        for i in range(n_pass):
+            decode_pass()
+            marks[i + 1].record()
+        torch.cuda.synchronize()
+        ev_end.synchronize()
+        w_end = ev_start.elapsed_time(ev_end)
+        inside = []
+        for i in range(n_pass):
+            a, b = ev_start.elapsed_time(marks[i]), ev_start.elapsed_time(marks[i + 1])
+            if a >= 0 and b <= w_end:
+                inside.append(b - a)
+        return h_, (sum(inside) / len(inside) * 1e-3 if inside else None), len(inside), host_ms
+
+    def start_out():
+        h_ = cache.swap_out(victims, host=host)
+        return h_, h_.out_start, h_.out_event
+
+    h, t_dec_out, n_dec, host_ms_out = under_swap(start_out)
     t_out = h.out_seconds()
-    t_dec_out = e0.elapsed_time(e1) * 1e-3 / max(n_dec, 1)
 
-    cache.swap_in(h)
-    n_dec_in = 0
-    e0.record()
-    while not h.in_event.query():
-        decode_pass()
-        n_dec_in += 1
-        torch.cuda.current_stream().synchronize()
-    e1.record()
-    h.in_event.synchronize()
-    torch.cuda.synchronize()
+    def start_in():
+        cache.swap_in(h)
+        return h, h.in_start, h.in_event
+
+    _, t_dec_in, n_dec_in, host_ms_in = under_swap(start_in)
     t_in = h.in_seconds()
-    t_dec_in = e0.elapsed_time(e1) * 1e-3 / max(n_dec_in, 1)
     after = cache.gather(0, victims)
     after_last = cache.gather(L - 1, victims)
     exact = all(torch.equal(a, b) for a, b in zip(before + before_last, after + after_last))
@@ -730,10 +745,15 @@ def run_cfg5(torch, seed, decode_steps=6):
            "decode_ms_alone": t_alone * 1e3,
            "decode_ms_during_swap_out": t_dec_out * 1e3 if n_dec else None,
            "decode_ms_during_swap_in": t_dec_in * 1e3 if n_dec_in else None,
-           "decode_steps_during_swap": n_dec + n_dec_in,
+           "decode_steps_during_swap_out": n_dec,
+           "decode_steps_during_swap_in": n_dec_in,
+           "host_ms_to_enqueue_swap": [round(host_ms_out, 3), round(host_ms_in, 3)],
            "restored_bit_exact": bool(exact)}
     sl = [x for x in (res["decode_ms_during_swap_out"], res["decode_ms_during_swap_in"]) if x]
     res["decode_slowdown"] = (sum(sl) / len(sl)) / res["decode_ms_alone"] if sl else None
+    for k in ("out", "in"):
+        x = res[f"decode_ms_during_swap_{k}"]
+        res[f"decode_slowdown_{k}"] = x / res["decode_ms_alone"] if x else None
     log(f"cfg5: swap out {res['swap_out_GBps']:.1f} GB/s, in {res['swap_in_GBps']:.1f} GB/s "
         f"({nbytes / 1e9:.2f} GB each way), decode slowdown {res['decode_slowdown']}, "
         f"restored exact {exact}")
@@ -841,6 +861,9 @@ def main():
         return
     if args.mode == "prefill3":
         print(json.dumps({"mode": "prefill3", **run_prefill(torch, args.seed)}), flush=True)
+        return
+    if args.mode == "swap5":
+        print(json.dumps({"mode": "swap5", **run_cfg5(torch, args.seed)}), flush=True)
         return
     if args.mode == "append3":
         print(json.dumps({"mode": "append3", **run_cfg3(torch, args.seed, layers=1)}), flush=True)
