@@ -67,8 +67,6 @@ constexpr int kReadGroup = 4;  // LDS reads scheduled together
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kLog2e = 1.44269504088896340736f;
 
-inline int64_t align4(int64_t n) { return (n + 3) / 4 * 4; }
-
 struct DecodeArgs {
   const uint16_t* q;
   int64_t q_stride;        // elements between requests
