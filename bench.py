@@ -40,6 +40,7 @@ Other modes used by the profiles (one kernel family each, few launches):
                   host memory) and swap preemption of a 4096-token request
   --mode swap5    configuration 5 swap out / swap in of 32 of 128 sequences
                   (16 layers) while the other 96 decode
+  --mode bs1      batch-1 latency at the reference's published decode shape
 """
 from __future__ import annotations
 
@@ -90,7 +91,7 @@ def parse_args():
                         "layer) instead of the fused append_and_decode")
     p.add_argument("--mode", default="step",
                    choices=["step", "copy", "decode2", "decode4", "append3", "prefill3",
-                            "xpacked", "offload", "swap5"])
+                            "xpacked", "offload", "swap5", "bs1"])
     return p.parse_args()
 
 
@@ -610,6 +611,64 @@ def run_offload(torch, seed, steps=3):
     return res
 
 
+def run_small_batch(torch, seed, layers=20, steps=50):
+    """Latency at the reference's own decode shape: Mixtral attention (Hkv 8,
+    Hq 32, D 128, page 16), batch 1, a 128-token context, 20 layers -- the
+    H100 figures it publishes are 90 us of FlashInfer decode per step and a
+    9.4 us decode-kernel median (src/MoE/tests/vLLM_comparison/README.md:102,
+    src/MoE/pipeline_parallelism.md:144) and 0.258 ms of step setup
+    (pipeline_parallelism.md:81).  Reported: the decode launch alone (event
+    time per launch over back-to-back launches), one step (setup + 20 fused
+    append + decode launches, event time), and the host time of the step
+    setup."""
+    from gpu_offloading_amd.kv_cache import PagedKVCache
+
+    cache = PagedKVCache(layers, 8, 128, max_seqs=1, max_seq_len=128 + steps + 64,
+                         num_qo_heads=32, kv_page_budget=64, device="cuda",
+                         workspace_bytes=1 << 22, staging_bytes=1 << 20)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 500)
+    cache.fill_kv_random(1.0, generator=g)
+    cache.ensure_pages(0, 128 // 16)
+    cache.advance([0], [128])
+    q = torch.randn(1, 32, 128, device="cuda", generator=g).to(torch.bfloat16)
+    nk = torch.randn(1, 8, 128, device="cuda", generator=g).to(torch.bfloat16)
+    nv = torch.randn_like(nk)
+    out = torch.empty_like(q)
+
+    def step():
+        cache.ensure_pages(0, (int(cache._seq_lens_cpu[0]) + 1 + 15) // 16)
+        t0 = time.perf_counter()
+        cache.prepare_decode_step([0])
+        setup = time.perf_counter() - t0
+        for layer in range(layers):
+            cache.append_and_decode(layer, nk, nv, q, out=out)
+        return setup
+
+    for _ in range(5):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    setups = []
+    e0.record()
+    for _ in range(steps):
+        setups.append(step())
+    e1.record()
+    torch.cuda.synchronize()
+    step_ms = e0.elapsed_time(e1) / steps
+    t_dec = _timed_rounds(torch, lambda: cache.decode(0, q, out=out), 100)
+    res = {"decode_launch_us": t_dec * 1e6, "step_ms_20_layers": step_ms,
+           "per_layer_us": step_ms * 1e3 / layers,
+           "step_setup_host_ms": 1e3 * sorted(setups)[len(setups) // 2],
+           "shape": "B=1, ctx 128 (+1 per step), Hkv 8, Hq 32, D 128, 20 layers"}
+    log(f"bs1: decode launch {res['decode_launch_us']:.1f} us, step {step_ms:.3f} ms for "
+        f"{layers} layers ({res['per_layer_us']:.1f} us/layer), setup "
+        f"{res['step_setup_host_ms']:.3f} ms host")
+    del cache
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_cfg4(torch, seed, reps=32, decode_only=False):
     """Configuration 4 (B=16 x 32768-token contexts): the median of three
     timed rounds of `reps` launches after a clock ramp (`decode_only`: the
@@ -862,6 +921,9 @@ def main():
     if args.mode == "prefill3":
         print(json.dumps({"mode": "prefill3", **run_prefill(torch, args.seed)}), flush=True)
         return
+    if args.mode == "bs1":
+        print(json.dumps({"mode": "bs1", **run_small_batch(torch, args.seed)}), flush=True)
+        return
     if args.mode == "swap5":
         print(json.dumps({"mode": "swap5", **run_cfg5(torch, args.seed)}), flush=True)
         return
@@ -878,6 +940,7 @@ def main():
         extra["f2_continuation_prefill"] = run_prefill(torch, args.seed)
         extra["f3_xpacked"] = run_xpacked(torch, args.seed)
         extra["f4_offload"] = run_offload(torch, args.seed)
+        extra["bs1_latency"] = run_small_batch(torch, args.seed)
     cpu = None if args.no_cpu else run_cpu_baseline(args.seed)
     line = {
         "metric": "paged decode-attn HBM GB/s (% peak) + KV append/gather/swap GB/s, 1 GPU",
