@@ -186,6 +186,27 @@ def check(func: str, status: int) -> None:
 
 def call(name: str, *args) -> int:
     """Call an int-status entry point and raise KvcError on failure."""
-    st = getattr(load(), name)(*args)
-    check(name, st)
+    lib = _lib if _lib is not None else load()   # no lock once loaded
+    st = getattr(lib, name)(*args)
+    if st != KVC_OK:
+        check(name, st)
     return st
+
+
+def current_stream_handle(device) -> int:
+    """hipStream_t (as an int) of torch's current stream on ``device``:
+    torch's raw-stream query when it has one (no Stream object is built),
+    else ``torch.cuda.current_stream(device).cuda_stream``."""
+    global _raw_stream
+    if _raw_stream is None:
+        import torch
+        fn = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+        if fn is None:
+            _raw_stream = lambda dev: torch.cuda.current_stream(dev).cuda_stream  # noqa: E731
+        else:
+            _raw_stream = lambda dev: fn(dev.index if dev.index is not None  # noqa: E731
+                                         else torch.cuda.current_device())
+    return _raw_stream(device)
+
+
+_raw_stream = None

@@ -17,6 +17,7 @@ step after bumping ``_seq_lens_cpu``, moe_engine.py:3554-3556).
 from __future__ import annotations
 
 import math
+import weakref
 from typing import Optional, Tuple, Union
 
 import numpy as np
@@ -71,6 +72,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
         self._num_indices = 0
         self._sm_scale = None
         self._plan_args = None
+        self._kv_checked = None   # (k ref, v ref, (ps, hkv, d), k geometry, v geometry)
 
     # ------------------------------------------------------------------ plan
     def plan(self, indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
@@ -244,7 +246,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
         if any(s not in (None, 1.0) for s in (q_scale, k_scale, v_scale)):
             _fail("q/k/v scales are not supported (bf16 cache)")
         k_cache, v_cache, out, lse = self._run_args(q, paged_kv_cache, out, lse, return_lse)
-        s = stream if stream is not None else torch.cuda.current_stream(self._device)
+        sh = (stream.cuda_stream if stream is not None
+              else _lib.current_stream_handle(self._device))
         ws = self._workspace
         _lib.call("kvc_batch_decode_run", self._sched, self._plan_dev.data_ptr(),
                   q.data_ptr(), q.stride(0),
@@ -252,7 +255,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
                   k_cache.shape[0], self._indptr.data_ptr(), self._indices.data_ptr(),
                   self._num_indices, self._lpl.data_ptr(), self._sm_scale, ws.data_ptr(),
                   ws.numel() * ws.element_size(), out.data_ptr(), out.stride(0),
-                  lse.data_ptr() if lse is not None else None, s.cuda_stream)
+                  lse.data_ptr() if lse is not None else None, sh)
         return (out, lse) if return_lse else out
 
     forward = run
@@ -287,7 +290,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
                 _fail(f"{name} must be bfloat16 [B, {hkv}, {d}] with contiguous heads")
             if t.device != self._device:
                 _fail(f"{name} on a different device than the workspace")
-        s = stream if stream is not None else torch.cuda.current_stream(self._device)
+        sh = (stream.cuda_stream if stream is not None
+              else _lib.current_stream_handle(self._device))
         ws = self._workspace
         _lib.call("kvc_batch_decode_append_run", self._sched, self._plan_dev.data_ptr(),
                   q.data_ptr(), q.stride(0),
@@ -296,7 +300,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
                   self._num_indices, self._lpl.data_ptr(), new_key.data_ptr(), new_key.stride(0),
                   new_value.data_ptr(), new_value.stride(0), self._sm_scale, ws.data_ptr(),
                   ws.numel() * ws.element_size(), out.data_ptr(), out.stride(0),
-                  lse.data_ptr() if lse is not None else None, s.cuda_stream)
+                  lse.data_ptr() if lse is not None else None, sh)
         return (out, lse) if return_lse else out
 
     def _run_args(self, q, paged_kv_cache, out, lse, return_lse):
@@ -310,6 +314,14 @@ class BatchDecodeWithPagedKVCacheWrapper:
             if paged_kv_cache.dim() != 5 or paged_kv_cache.shape[1] != 2:
                 _fail("a single paged_kv_cache tensor must be [pages, 2, page_size, heads, dim]")
             k_cache, v_cache = paged_kv_cache[:, 0], paged_kv_cache[:, 1]
+        # The per-layer cache views are the same tensor objects call after
+        # call: once checked against this (page_size, heads, dim) they are
+        # only compared by identity, shape and strides.
+        seen = self._kv_checked
+        if (seen is not None and seen[0]() is k_cache and seen[1]() is v_cache
+                and seen[2] == (ps, hkv, d) and seen[3] == (k_cache.shape, k_cache.stride())
+                and seen[4] == (v_cache.shape, v_cache.stride())):
+            return k_cache, v_cache, *self._out_args(q, out, lse, return_lse)
         for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
             if c.dim() != 4 or tuple(c.shape[1:]) != (ps, hkv, d):
                 _fail(f"{name} must be [pages, {ps}, {hkv}, {d}], got {tuple(c.shape)}")
@@ -321,6 +333,13 @@ class BatchDecodeWithPagedKVCacheWrapper:
                 _fail(f"{name} on {c.device}, workspace on {self._device}")
         if k_cache.stride() != v_cache.stride() or k_cache.shape[0] != v_cache.shape[0]:
             _fail("k_cache and v_cache must share shape and strides")
+        self._kv_checked = (weakref.ref(k_cache), weakref.ref(v_cache), (ps, hkv, d),
+                            (k_cache.shape, k_cache.stride()), (v_cache.shape, v_cache.stride()))
+        return k_cache, v_cache, *self._out_args(q, out, lse, return_lse)
+
+    def _out_args(self, q, out, lse, return_lse):
+        """Check q against the plan; allocate or check out / lse."""
+        batch, hq, hkv, d, ps = self._plan_args
         if q.dim() != 3 or q.shape[0] < batch or tuple(q.shape[1:]) != (hq, d):
             _fail(f"q must be [{batch}, {hq}, {d}], got {tuple(q.shape)}")
         if q.dtype != torch.bfloat16 or q.stride(2) != 1 or q.stride(1) != d:
@@ -337,7 +356,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
         if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()
                                 or lse.numel() < batch * hq):
             _fail("lse must be contiguous float32 [B, num_qo_heads]")
-        return k_cache, v_cache, out, lse
+        return out, lse
 
     def end_forward(self) -> None:
         """No-op kept for interface parity."""

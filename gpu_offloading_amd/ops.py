@@ -44,8 +44,7 @@ def _fail(msg: str) -> None:
 
 
 def _stream_handle(device: torch.device, stream: Optional[torch.cuda.Stream]) -> int:
-    s = stream if stream is not None else torch.cuda.current_stream(device)
-    return s.cuda_stream
+    return stream.cuda_stream if stream is not None else _lib.current_stream_handle(device)
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:

@@ -179,13 +179,14 @@ class BatchPrefillWithPagedKVCacheWrapper:
         if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()
                                 or lse.numel() < total_q * hq):
             _fail("lse must be contiguous float32 [total_q, num_qo_heads]")
-        s = stream if stream is not None else torch.cuda.current_stream(self._device)
+        sh = (stream.cuda_stream if stream is not None
+              else _lib.current_stream_handle(self._device))
         _lib.call("kvc_batch_prefill_run", self._sched, self._plan_dev.data_ptr(),
                   q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
                   k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
                   self._indices.data_ptr(), self._indices.numel(), self._sm_scale,
                   out.data_ptr(), out.stride(0),
-                  lse.data_ptr() if lse is not None else None, s.cuda_stream)
+                  lse.data_ptr() if lse is not None else None, sh)
         return (out, lse) if return_lse else out
 
     forward = run
