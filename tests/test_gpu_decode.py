@@ -195,6 +195,27 @@ def test_decode_cfg4_long_context(gpu):
         assert_attn_close(got[sl], ref)
 
 
+def test_decode_cfg5_mha_batch(gpu):
+    """Config 5's decode shape: OLMoE attention (MHA, 16 heads), 128
+    requests x 2048 tokens from a shuffled 16,384-page pool; six requests
+    (first, last and four inside) are checked against the oracle."""
+    cfg = workloads.config5(seed=0)
+    lens = [ln + 1 for ln in cfg.seq_lens]       # the step's own token is attended
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, 16, 128, 18, device=gpu)
+    q = randn_bf16((len(lens), 16, 128), 19, device=gpu)
+    (out, lse), w = _run(gpu, q, kc, vc, indptr, indices, lpl, 16, 16, 128)
+    assert w.schedule.max_partitions > 1
+    kcn, vcn = u16(kc), u16(vc)
+    got = out.float().cpu().numpy()
+    for b in (0, 17, 63, 64, 100, 127):
+        sl = slice(b, b + 1)
+        ip = indptr[sl.start:sl.stop + 1] - indptr[b]
+        idx = indices[indptr[b]:indptr[b + 1]]
+        ref, ref_lse = orc.paged_decode(u16(q[sl]), kcn, vcn, ip, idx, lpl[sl])
+        assert_attn_close(got[sl], ref)
+        assert np.abs(lse[sl].cpu().numpy() - ref_lse).max() < 2e-3
+
+
 def test_merge_attention_states_matches_oracle(gpu):
     o1 = randn_bf16((5, 32, 128), 20, device=gpu)
     o2 = randn_bf16((5, 32, 128), 21, device=gpu)
