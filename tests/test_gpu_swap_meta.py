@@ -172,3 +172,42 @@ def test_cache_swap_chunks_across_layers_bit_exact(gpu, staging_blocks):
     for l in range(layers):
         assert torch.equal(cache.k_cache[l][torch.from_numpy(pages[1]).long().to(gpu)], keep1[l])
     assert [int(cache._seq_lens_cpu[s]) for s in (3, 0, 1, 2)] == [70, 64, 40, 0]
+
+
+def test_cfg5_swap_under_decode_round_trip(gpu):
+    """Configuration 5's shape (OLMoE MHA 16 x 128, 128 requests x 2048
+    tokens on a shuffled 16,384-page pool; 4 of its 16 layers): a seeded
+    25% of the requests are swapped out while the other 96 decode, then
+    swapped back into other slots; the restored pages are bit-exact and
+    the decode of the running requests is unchanged by the swap."""
+    from gpu_offloading_amd.kv_cache import PagedKVCache
+
+    cfg = workloads.config5(seed=0)
+    L, B = 4, len(cfg.seq_lens)
+    cache = PagedKVCache(L, 16, 128, max_seqs=B + 32, max_seq_len=2048 + 64, num_qo_heads=16,
+                         kv_page_budget=cfg.total_pages, free_page_order=cfg.free_order,
+                         device=gpu, staging_bytes=256 << 20)
+    seqs = list(range(B))
+    for s in seqs:
+        cache.ensure_pages(s, 2048 // 16)
+    cache.advance(seqs, cfg.seq_lens)
+    cache.fill_kv_random(1.0, generator=torch.Generator(device=gpu).manual_seed(90))
+    victims = sorted(workloads.randperm(B, 7)[: B // 4])
+    running = [s for s in seqs if s not in set(victims)]
+    before = [cache.gather(layer, victims) for layer in range(L)]
+    q = torch.randn(len(running), 16, 128, generator=torch.Generator(device=gpu).manual_seed(91),
+                    device=gpu).to(torch.bfloat16)
+    cache.plan_decode(running)
+    ref = [cache.decode(layer, q).clone() for layer in range(L)]
+    h = cache.swap_out(victims)
+    during = [cache.decode(layer, q) for layer in range(L)]
+    cache.synchronize_swaps()
+    targets = list(range(B, B + len(victims)))          # resume in other slots
+    cache.swap_in(h, seq_ids=targets, wait=True)
+    after = [cache.gather(layer, targets) for layer in range(L)]
+    torch.cuda.synchronize()
+    for layer in range(L):
+        assert torch.equal(during[layer], ref[layer])
+        for a, b in zip(before[layer], after[layer]):
+            assert torch.equal(a, b)
+    assert h.bytes_per_direction == L * len(victims) * 128 * 2 * 16 * 16 * 128 * 2
