@@ -204,3 +204,38 @@ def test_xpacked_rejects_bad_inputs(gpu):
     with pytest.raises(RuntimeError, match="block-sparse"):
         ops.paged_attention_v1(out, q, kc, vc, 2, 0.1, bt, sl, 16, 20, None, "auto", 1.0, 1.0,
                                0, 4, 0, 64, 0)
+
+
+def _torch_ref(q, kc, vc, bt, lens, scale):
+    """fp32 attention per sequence over the x-packed caches, unpacked on the
+    GPU through the layout's closed form (k[tok, h, d] = kc[blk, h, d // 8,
+    tok, d % 8]; v[tok, h, d] = vc[blk, h, d, tok])."""
+    outs = []
+    for b, n in enumerate(lens):
+        blocks = torch.from_numpy(bt[b, :(n + 15) // 16].astype(np.int64)).to(q.device)
+        k = kc[blocks].permute(0, 3, 1, 2, 4).reshape(-1, kc.shape[1], 128)[:n].float()
+        v = vc[blocks].permute(0, 3, 1, 2).reshape(-1, vc.shape[1], 128)[:n].float()
+        s = torch.matmul(k.permute(1, 0, 2).contiguous(), q[b].float()[:, :, None])[..., 0] * scale
+        p = torch.softmax(s, dim=-1)                                   # [H, n]
+        outs.append(torch.matmul(p[:, None, :], v.permute(1, 0, 2).contiguous())[:, 0])
+    return torch.stack(outs)
+
+
+@pytest.mark.parametrize("case", ["1x150000", "64xU512_4096"])
+def test_xpacked_at_the_bench_shapes(gpu, case):
+    """The benchmark's x-packed shapes (MHA 32 x 128, fp16): one 150,000-token
+    sequence (the reference's GH200 point) and 64 sequences of U[512, 4096]
+    tokens; v2 (and v1 for the long sequence) against an fp32 reference."""
+    rng = np.random.default_rng(64)
+    lens = [150_000] if case == "1x150000" else rng.integers(512, 4097, 64).tolist()
+    q, kc, vc, bt = _attn_case(lens, 32, 32, "fp16", 65, gpu)
+    scale = 1 / np.sqrt(128)
+    ref = _torch_ref(q, kc, vc, bt, lens, scale).cpu().numpy()
+    out, *_ = _run_v2(q, kc, vc, bt, lens, 32, scale, gpu)
+    assert_attn_close(out.float().cpu().numpy(), ref)
+    if case == "1x150000":
+        out1 = torch.empty_like(q)
+        ops.paged_attention_v1(out1, q, kc, vc, 32, scale, torch.from_numpy(bt).to(gpu),
+                               torch.tensor(lens, dtype=torch.int32, device=gpu), 16,
+                               max(lens), None, "auto", torch.tensor(1.0), torch.tensor(1.0))
+        assert_attn_close(out1.float().cpu().numpy(), ref)
