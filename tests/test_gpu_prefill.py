@@ -167,3 +167,27 @@ def test_cache_continuation_prefill_flow(gpu):
                                          qo, kvi, idx, lpl, causal=True)
         assert_attn_close(out.float().cpu().numpy(), ref)
         assert np.abs(lse.cpu().numpy() - ref_lse).max() < 2e-3
+
+
+@pytest.mark.parametrize("kv_len", [2048, 4096])
+def test_prefill_at_the_bench_shape(gpu, kv_len):
+    """The benchmark's continuation prefill: 8 requests x 2048-token chunks
+    at the tail of 2048 / 4096 cached tokens, Mixtral heads (32 / 8), causal;
+    against fp32 torch SDPA with its lower-right causal mask, on the GPU."""
+    from torch.nn.attention.bias import causal_lower_right
+
+    q_lens, kv_lens = [2048] * 8, [kv_len] * 8
+    q, kc, vc, qo, kvi, idx, lpl = _case(q_lens, kv_lens, 32, 8, 50, device=gpu)
+    (out, lse), _ = _run(gpu, q, kc, vc, qo, kvi, idx, lpl, 32, 8)
+    kg, vg = kc.to(gpu), vc.to(gpu)
+    for b in range(8):
+        pages = torch.from_numpy(idx[kvi[b]:kvi[b + 1]].astype(np.int64)).to(gpu)
+        k = kg[pages].flatten(0, 1)[:kv_len].float().permute(1, 0, 2)   # [Hkv, n, D]
+        v = vg[pages].flatten(0, 1)[:kv_len].float().permute(1, 0, 2)
+        k = k.repeat_interleave(4, 0).contiguous()
+        v = v.repeat_interleave(4, 0).contiguous()
+        qb = q[qo[b]:qo[b + 1]].float().permute(1, 0, 2).contiguous()  # [Hq, 2048, D]
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            qb, k, v, attn_mask=causal_lower_right(2048, kv_len))
+        assert_attn_close(out[qo[b]:qo[b + 1]].float().cpu().numpy(),
+                          ref.permute(1, 0, 2).cpu().numpy())
