@@ -244,3 +244,24 @@ def test_decode_split_merge_equals_whole(gpu):
                        lpl, 32, 8, 128)
     merged, _ = ops.merge_attention_states(o1, l1, o2, l2)
     assert_attn_close(merged.float().cpu().numpy(), whole.float().cpu().numpy())
+
+
+def test_run_rechecks_caches_after_a_new_plan(gpu):
+    """run() checks a cache tensor once per (tensor, plan geometry): a plan
+    for other head counts makes the same tensors fail again, and a tensor
+    of the wrong geometry is refused even after good ones were accepted."""
+    lens = [40, 100]
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, 8, 128, 21, device=gpu)
+    q = randn_bf16((2, 32, 128), 22, device=gpu)
+    out1, w = _run(gpu, q, kc, vc, indptr, indices, lpl, 32, 8, 128, return_lse=False)
+    out2 = w.run(q, (kc, vc))                          # cached check, same result
+    assert torch.equal(out1, out2)
+    w.plan(torch.from_numpy(indptr), torch.from_numpy(indices).to(gpu), torch.from_numpy(lpl),
+           num_qo_heads=16, num_kv_heads=4, head_dim=128, page_size=16)
+    with pytest.raises(RuntimeError, match="k_cache must be"):
+        w.run(randn_bf16((2, 16, 128), 23, device=gpu), (kc, vc))
+    w.plan(torch.from_numpy(indptr), torch.from_numpy(indices).to(gpu), torch.from_numpy(lpl),
+           num_qo_heads=32, num_kv_heads=8, head_dim=128, page_size=16)
+    assert torch.equal(w.run(q, (kc, vc)), out1)
+    with pytest.raises(RuntimeError, match="v_cache must be bfloat16"):
+        w.run(q, (kc, vc.half()))
