@@ -90,7 +90,7 @@ SIGNATURES = {
     "kvc_gather_kv": (c_int, [
         _P, _P, _I32P, c_int64, c_int32, _I32P, _I32P,
         c_int32, c_int32, c_int32, c_int32, c_int32, c_int64, c_int32,
-        c_int64, c_int64, _P, _P, c_int64, _I32P, _P]),
+        c_int64, c_int64, _P, _P, c_int64, c_int64, _I32P, _P]),
     "kvc_decode_plan_ints": (c_int64, [c_int32, c_int32]),
     "kvc_decode_plan": (c_int, [
         c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
@@ -135,7 +135,7 @@ SIGNATURES = {
         _I32P, c_int64, c_int32, c_int32, _I32P, _I32P, _I32P,
         c_int32, c_int32, c_int32, c_int32, _P, _I32P, _P]),
     "kvc_copy_page_indices": (c_int, [
-        _I32P, c_int64, c_int32, _I32P, _I32P, c_int32, c_int32, _I32P, _P]),
+        _I32P, c_int64, c_int32, _I32P, _I32P, c_int32, c_int32, _I32P, c_int64, _P]),
 }
 
 _lock = threading.Lock()

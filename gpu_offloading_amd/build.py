@@ -44,19 +44,44 @@ def sources() -> list[str]:
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
-def build_library(verbose: bool = False) -> str:
-    """Compile every csrc/*.hip into libkvc.so (always recompiles)."""
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}",
-           *sources(), "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+def _run(cmd: list[str]) -> tuple[int, list[str]]:
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "'-packed-fp32-ops' is not a recognized feature"
-    msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if noise not in ln]
-    if res.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
+    return res.returncode, [ln for ln in (res.stdout + res.stderr).splitlines()
+                            if noise not in ln]
+
+
+def build_library(verbose: bool = False, jobs: int | None = None) -> str:
+    """Compile every csrc/*.hip into libkvc.so (always recompiles): one hipcc
+    process per source file, in parallel, then one link."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    os.makedirs(LIB_DIR, exist_ok=True)
+    obj_dir = os.path.join(LIB_DIR, "obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    srcs = sources()
+    objs = [os.path.join(obj_dir, os.path.basename(s)[:-4] + ".o") for s in srcs]
+    cmds = [[hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", s, "-o", o]
+            for s, o in zip(srcs, objs)]
+    jobs = jobs or min(len(cmds), max(1, min(os.cpu_count() or 1, 16)))
+    if verbose:
+        for c in cmds:
+            print(" ".join(c), flush=True)
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        results = list(ex.map(_run, cmds))
+    failed = [(s, m) for s, (rc, m) in zip(srcs, results) if rc != 0]
+    if failed:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(
+            f"{s}:\n" + "\n".join(m) for s, m in failed))
+    msgs = [ln for _, m in results for ln in m]
+    tmp = LIB_PATH + ".tmp"
+    link = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    if verbose:
+        print(" ".join(link), flush=True)
+    rc, lm = _run(link)
+    if rc != 0:
+        raise RuntimeError("hipcc link failed:\n" + "\n".join(lm))
+    msgs += lm
     if verbose and msgs:
         print("\n".join(msgs), file=sys.stderr)
     os.replace(tmp, LIB_PATH)

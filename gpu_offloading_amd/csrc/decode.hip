@@ -756,6 +756,11 @@ __device__ __forceinline__ float wave_sum(float v) {
 // every lane folds its D/64 dims.  Requests with a single piece were finished
 // by the streaming kernel; requests with no pages get a zero output and
 // lse = -inf.
+//
+// With no split request in the batch (max_parts == 1) the launch only zeroes
+// the empty requests and the workspace is absent (part_o == part_lse ==
+// null): then no partial is read, and every request counts at most one
+// piece.
 constexpr int kSpecParts = 16;
 
 template <int D>
@@ -768,20 +773,24 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
   const int Hq = a.num_kv_heads * G;
   const int h = hq / G;
   const int g = hq - h * G;
-  const int64_t base = (int64_t(b) * a.num_kv_heads + h) * a.max_parts;
-  const float* lp = a.part_lse + base * G + g;  // piece p at lp[p * G]
+  const bool have_parts = a.part_o != nullptr && a.part_lse != nullptr;  // uniform
+  const int max_parts = have_parts ? a.max_parts : 1;
+  const int64_t base = (int64_t(b) * a.num_kv_heads + h) * max_parts;
+  const int64_t lse0 = base * G + g;  // piece p at part_lse[lse0 + p * G]
   const int nparts_raw = a.req_nparts[b];
-  const int nspec = min(a.max_parts, kSpecParts);
-  const float lse_spec = lane < min(a.max_parts, 64) ? lp[int64_t(lane) * G] : -INFINITY;
+  const int nspec = have_parts ? min(max_parts, kSpecParts) : 0;
+  const float lse_spec = (have_parts && lane < min(max_parts, 64))
+                             ? a.part_lse[lse0 + int64_t(lane) * G] : -INFINITY;
   float po[kSpecParts][EPL];
 #pragma unroll
   for (int p = 0; p < kSpecParts; ++p) {
-    const float* src = a.part_o + ((base + p) * G + g) * D + lane * EPL;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) po[p][e] = p < nspec ? src[e] : 0.f;
+    for (int e = 0; e < EPL; ++e)
+      po[p][e] = p < nspec ? a.part_o[((base + p) * G + g) * D + lane * EPL + e] : 0.f;
   }
-  const int nparts = min(nparts_raw, a.max_parts);
+  const int nparts = min(nparts_raw, max_parts);
   if (nparts == 1) return;
+  const float* lp = have_parts ? a.part_lse + lse0 : nullptr;  // read only when nparts > 64
   uint16_t* out = a.out + int64_t(b) * a.out_stride + int64_t(hq) * D;
 
   float mx = lane < nparts ? lse_spec : -INFINITY;
@@ -1057,8 +1066,9 @@ int decode_run(const kvc_decode_schedule* sched, const int32_t* plan, const void
   KVC_REQUIRE(sched, KVC_ERR_INVALID_ARG, "null schedule");
   const int batch = sched->batch;
   if (batch == 0) return ok();
-  KVC_REQUIRE(plan && q && key_cache && value_cache && indptr && indices &&
-                  last_page_len && out,
+  // indices may be null (an empty tensor) when no request has a page.
+  KVC_REQUIRE(plan && q && key_cache && value_cache && indptr &&
+                  (indices || sched->total_pages == 0) && last_page_len && out,
               KVC_ERR_INVALID_ARG, "null pointer");
   const int Hq = sched->num_qo_heads, Hkv = sched->num_kv_heads, D = sched->head_dim;
   KVC_REQUIRE(Hkv > 0 && Hq % Hkv == 0, KVC_ERR_INVALID_ARG, "bad head counts");
@@ -1118,6 +1128,11 @@ int decode_run(const kvc_decode_schedule* sched, const int32_t* plan, const void
   a.part_lse = need ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                               (rows * D * 4 + 255) / 256 * 256)
                     : nullptr;
+  // Partials are written (streaming kernel) and read (merge) only for split
+  // requests, which exist only when max_partitions > 1; with one piece per
+  // request both kernels get null partials and never touch them.
+  KVC_REQUIRE(sched->max_partitions == 1 || (a.part_o && a.part_lse), KVC_ERR_WORKSPACE,
+              "a plan with split requests needs the partials workspace");
   a.out = static_cast<uint16_t*>(out);
   a.out_stride = out_batch_stride;
   a.lse = lse;

@@ -35,6 +35,7 @@ struct GatherArgs {
   char* out_key;
   char* out_value;
   int64_t out_stride;         // bytes between output rows
+  int64_t out_rows;           // rows the outputs hold; rows past them are not written
   int32_t block_size;
   int32_t row_units;          // 16-byte chunks (or elements) per row
   int32_t* oob_count;
@@ -66,12 +67,16 @@ __global__ __launch_bounds__(kThreads) void gather_vec16_kernel(GatherArgs a) {
       const uint32_t rem = item - t * per_tok;
       const bool is_v = rem >= rc;
       const uint32_t chunk = is_v ? rem - rc : rem;
+      const int64_t orow = int64_t(row0) + i0 + int(t);
+      if (orow < 0 || orow >= a.out_rows) {
+        if (a.oob_count && chunk == 0 && !is_v) atomicAdd(a.oob_count, 1);
+        continue;
+      }
       const int pos = start + i0 + int(t);
       const int page = pos >= 0 ? pos / a.block_size : -1;
       const int32_t blk = (page >= 0 && page < a.bt_width) ? bt_row[page] : -1;
       const int off = pos - page * a.block_size;
-      dst[u] = (is_v ? a.out_value : a.out_key) +
-               int64_t(row0 + i0 + int(t)) * a.out_stride + chunk * 16u;
+      dst[u] = (is_v ? a.out_value : a.out_key) + orow * a.out_stride + chunk * 16u;
       if (blk < 0 || blk >= a.num_blocks) {
         buf[u] = make_uint4(0, 0, 0, 0);
         if (a.oob_count && chunk == 0 && !is_v) atomicAdd(a.oob_count, 1);
@@ -106,12 +111,16 @@ __global__ __launch_bounds__(kThreads) void gather_elem_kernel(GatherArgs a) {
     const uint32_t rem = item - t * per_tok;
     const bool is_v = rem >= re;
     const uint32_t e = is_v ? rem - re : rem;
+    const int64_t orow = int64_t(row0) + i0 + int(t);
+    if (orow < 0 || orow >= a.out_rows) {
+      if (a.oob_count && e == 0 && !is_v) atomicAdd(a.oob_count, 1);
+      continue;
+    }
     const int pos = start + i0 + int(t);
     const int page = pos >= 0 ? pos / a.block_size : -1;
     const int32_t blk = (page >= 0 && page < a.bt_width) ? bt_row[page] : -1;
     const int off = pos - page * a.block_size;
-    T* dst = reinterpret_cast<T*>((is_v ? a.out_value : a.out_key) +
-                                  int64_t(row0 + i0 + int(t)) * a.out_stride);
+    T* dst = reinterpret_cast<T*>((is_v ? a.out_value : a.out_key) + orow * a.out_stride);
     if (blk < 0 || blk >= a.num_blocks) {
       dst[e] = T(0);
       if (a.oob_count && e == 0 && !is_v) atomicAdd(a.oob_count, 1);
@@ -137,9 +146,9 @@ extern "C" int kvc_gather_kv(
     int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
     int64_t num_blocks, int32_t elem_bytes, int64_t cache_block_stride,
     int64_t cache_token_stride, void* out_key, void* out_value,
-    int64_t out_token_stride, int32_t* oob_count, void* stream) {
-  KVC_REQUIRE(batch >= 0 && max_seq_len >= 0, KVC_ERR_INVALID_ARG,
-              "negative batch or max_seq_len");
+    int64_t out_token_stride, int64_t out_rows, int32_t* oob_count, void* stream) {
+  KVC_REQUIRE(batch >= 0 && max_seq_len >= 0 && out_rows >= 0, KVC_ERR_INVALID_ARG,
+              "negative batch, max_seq_len or out_rows");
   if (batch == 0 || max_seq_len == 0) return ok();
   KVC_REQUIRE(key_cache && value_cache && block_table && cu_seq_lens &&
                   out_key && out_value,
@@ -172,6 +181,7 @@ extern "C" int kvc_gather_kv(
   a.out_key = static_cast<char*>(out_key);
   a.out_value = static_cast<char*>(out_value);
   a.out_stride = out_token_stride * elem_bytes;
+  a.out_rows = out_rows;
   a.block_size = block_size;
   a.oob_count = oob_count;
   hipStream_t s = static_cast<hipStream_t>(stream);

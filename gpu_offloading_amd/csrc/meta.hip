@@ -9,7 +9,8 @@
 //
 // kvc_copy_page_indices restates _copy_page_indices_kernel after the row
 // index_select (moe_engine.py:1937-1946): the first indptr[r+1]-indptr[r]
-// entries of block-table row seq_ids[r] are flattened into indices[indptr[r]:].
+// entries of block-table row seq_ids[r] are flattened into indices[indptr[r]:]
+// (clamped to the buffer's capacity).
 #include "kvc_common.h"
 
 #include <algorithm>
@@ -67,12 +68,15 @@ __global__ __launch_bounds__(256) void slot_mapping_kernel(SlotArgs a) {
 
 __global__ __launch_bounds__(256) void copy_page_indices_kernel(
     const int32_t* bt, int64_t bt_stride, int32_t rows, const int32_t* seq_ids,
-    const int32_t* indptr, int32_t width, int32_t* indices) {
+    const int32_t* indptr, int32_t width, int32_t* indices, int64_t capacity) {
   const int r = blockIdx.x;
   const int row = seq_ids ? seq_ids[r] : r;
   if (row < 0 || row >= rows) return;
   const int beg = indptr[r];
-  const int n = min(indptr[r + 1] - beg, width);
+  if (beg < 0) return;
+  // Entries past the indices buffer (an indptr larger than the buffer) are
+  // not written.
+  const int n = int(min<int64_t>(min(indptr[r + 1] - beg, width), capacity - beg));
   const int32_t* src = bt + int64_t(row) * bt_stride;
   for (int j = threadIdx.x; j < n; j += 256) indices[beg + j] = src[j];
 }
@@ -111,8 +115,10 @@ extern "C" int kvc_copy_page_indices(const int32_t* block_table,
                                      int32_t block_table_rows,
                                      const int32_t* seq_ids, const int32_t* indptr,
                                      int32_t num_reqs, int32_t max_pages_per_req,
-                                     int32_t* indices, void* stream) {
-  KVC_REQUIRE(num_reqs >= 0, KVC_ERR_INVALID_ARG, "num_reqs < 0");
+                                     int32_t* indices, int64_t indices_capacity,
+                                     void* stream) {
+  KVC_REQUIRE(num_reqs >= 0 && indices_capacity >= 0, KVC_ERR_INVALID_ARG,
+              "num_reqs or indices_capacity < 0");
   if (num_reqs == 0) return ok();
   KVC_REQUIRE(block_table && indptr && indices, KVC_ERR_INVALID_ARG, "null pointer");
   KVC_REQUIRE(block_table_rows > 0 && max_pages_per_req > 0, KVC_ERR_INVALID_ARG,
@@ -120,7 +126,7 @@ extern "C" int kvc_copy_page_indices(const int32_t* block_table,
   copy_page_indices_kernel<<<dim3(unsigned(num_reqs)), 256, 0,
                              static_cast<hipStream_t>(stream)>>>(
       block_table, block_table_row_stride, block_table_rows, seq_ids, indptr,
-      max_pages_per_req, indices);
+      max_pages_per_req, indices, indices_capacity);
   KVC_LAUNCH_CHECK();
   return ok();
 }

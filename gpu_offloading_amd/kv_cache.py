@@ -272,10 +272,18 @@ class PagedKVCache:
         return self._pool.seq_pages(seq_id)
 
     def free_seq(self, seq_id: int) -> None:
-        """moe_engine.py:4212-4227: seq_len -> 0 and (dynamic) pages freed."""
+        """moe_engine.py:4212-4227: seq_len -> 0 and (dynamic) pages freed.
+
+        A restore of this sequence still in flight on the side stream keeps
+        writing its pages: the current stream first waits for it, so that
+        whoever is given the pages next (an append on the current stream, a
+        swap on the side stream, which waits for the current one) writes
+        after the restore."""
+        ev = self._pending_in.pop(seq_id, None)
+        if ev is not None:
+            torch.cuda.current_stream(self.device).wait_event(ev)
         self._seq_lens_cpu[seq_id] = 0
         self.seq_lens[seq_id] = 0
-        self._pending_in.pop(seq_id, None)
         if self._dynamic_pages:
             self.free_seq_pages(seq_id)
 
@@ -312,6 +320,23 @@ class PagedKVCache:
             vc.copy_(s)
 
     # --------------------------------------------------------- step metadata
+    def _check_seq_ids(self, seq_ids: Sequence[int]) -> np.ndarray:
+        """``seq_ids`` as int64, after checking they are distinct rows of the
+        block table (a negative id would wrap in numpy indexing, and a
+        repeated one could size the page list past its device buffer)."""
+        ids = np.asarray(seq_ids, dtype=np.int64).reshape(-1)
+        if len(ids) and (ids.min() < 0 or ids.max() >= self.max_seqs
+                         or len(np.unique(ids)) != len(ids)):
+            raise ValueError(f"seq_ids must be distinct and in [0, {self.max_seqs})")
+        return ids
+
+    def _check_page_counts(self, nblk: np.ndarray) -> None:
+        """Every planned sequence fits its block-table row, so the flattened
+        page list of distinct sequences fits the device index buffer."""
+        if len(nblk) and int(nblk.max()) > self.max_pages_per_seq:
+            raise RuntimeError(f"a sequence holds more than max_seq_len "
+                               f"({self.max_pages_per_seq * self.page_size}) tokens")
+
     def _sync_seqs(self, seq_ids: Sequence[int]) -> None:
         """Order the current stream after pending swap-ins of these sequences."""
         if not self._pending_in:
@@ -360,17 +385,18 @@ class PagedKVCache:
         page indices flattened on the device, then ``wrapper.plan``."""
         self._require_gpu()
         self._step_slots = None
-        b = len(seq_ids)
+        ids = self._check_seq_ids(seq_ids)
+        b = len(ids)
         if b == 0:
             return
         self._sync_seqs(seq_ids)
-        ids = np.asarray(seq_ids, dtype=np.int64)
         lens = self._seq_lens_cpu.numpy()[ids].astype(np.int32)
         nblk = (lens + self.page_size - 1) // self.page_size
         indptr = np.zeros(b + 1, dtype=np.int32)
         np.cumsum(nblk, out=indptr[1:])
         lpl = lens % self.page_size
         lpl = np.where((lpl == 0) & (lens != 0), self.page_size, lpl).astype(np.int32)
+        self._check_page_counts(nblk)
         indptr_d = self._to_device(indptr)
         ids_d = self._to_device(ids.astype(np.int32))
         ops.copy_page_indices(self.block_table, indptr_d, self._plan_indices_gpu, seq_ids=ids_d)
@@ -387,11 +413,11 @@ class PagedKVCache:
         causal against everything cached)."""
         self._require_gpu()
         self._step_slots = None
-        b = len(seq_ids)
+        ids = self._check_seq_ids(seq_ids)
+        b = len(ids)
         if len(chunk_lens) != b:
             raise ValueError("one chunk length per sequence")
         self._sync_seqs(seq_ids)
-        ids = np.asarray(seq_ids, dtype=np.int64)
         lens = self._seq_lens_cpu.numpy()[ids].astype(np.int64)
         clen = np.asarray(chunk_lens, dtype=np.int64)
         if (clen < 0).any() or (clen > lens).any():
@@ -403,6 +429,7 @@ class PagedKVCache:
         np.cumsum(clen, out=qo_indptr[1:])
         lpl = lens % self.page_size
         lpl = np.where((lpl == 0) & (lens != 0), self.page_size, lpl).astype(np.int32)
+        self._check_page_counts(nblk)
         ops.copy_page_indices(self.block_table, self._to_device(kv_indptr),
                               self._prefill_indices_gpu, seq_ids=self._to_device(ids.astype(np.int32)))
         total = int(kv_indptr[b])
@@ -446,12 +473,10 @@ class PagedKVCache:
             # Nothing to plan, or an error for slot_mapping to report.
             slots = self.slot_mapping(seq_ids, [1] * b, graph_n)
             return slots
+        ids = self._check_seq_ids(seq_ids)
         self._sync_seqs(seq_ids)
-        ids = np.asarray(seq_ids, dtype=np.int64)
         lens_all = self._seq_lens_cpu.numpy()
         ms, ps = self.max_seqs, self.page_size
-        if ids.min() < 0 or ids.max() >= ms or len(np.unique(ids)) != b:
-            raise ValueError(f"seq_ids must be distinct and in [0, {ms})")
         lens = lens_all[ids].astype(np.int32) + 1
         if int(lens.max()) > self.max_pages_per_seq * ps:
             raise RuntimeError(f"a sequence would exceed max_seq_len ({self.max_pages_per_seq * ps})")
@@ -557,19 +582,24 @@ class PagedKVCache:
         """Contiguous ``[sum(len), heads, dim]`` K and V of the given sequences
         (their current ``seq_lens``), in order."""
         self._require_gpu()
+        ids = self._check_seq_ids(seq_ids)
         self._sync_seqs(seq_ids)
-        ids = np.asarray(seq_ids, dtype=np.int64)
         lens = self._seq_lens_cpu.numpy()[ids].astype(np.int32)
         cu = np.zeros(len(ids) + 1, dtype=np.int32)
         np.cumsum(lens, out=cu[1:])
+        total = int(cu[-1])
+        for name, t in (("out_key", out_key), ("out_value", out_value)):
+            if t is not None and (t.dim() < 1 or t.shape[0] < total):
+                raise RuntimeError(f"{name} holds {t.shape[0] if t.dim() else 0} rows; "
+                                   f"the sequences have {total} tokens")
         cu_t = self._to_device(cu)
         rows = self.block_table.index_select(0, self._to_device(ids))
-        total = int(cu[-1])
         if out_key is None:
             out_key = torch.empty(total, self.num_kv_heads, self.head_dim, dtype=self.dtype,
                                   device=self.device)
         if out_value is None:
-            out_value = torch.empty_like(out_key)
+            out_value = torch.empty(total, self.num_kv_heads, self.head_dim, dtype=self.dtype,
+                                    device=self.device)
         return ops.gather_kv(self.k_cache[layer], self.v_cache[layer], rows, cu_t,
                              int(lens.max()) if len(lens) else 0, out_key, out_value)
 

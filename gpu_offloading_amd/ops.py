@@ -174,12 +174,15 @@ def gather_kv(key_cache: torch.Tensor, value_cache: torch.Tensor,
             _fail(f"{name} dtype {t.dtype} != cache dtype {key_cache.dtype}")
     if out_key.stride(0) != out_value.stride(0):
         _fail("out_key and out_value must share the token stride")
+    # The kernel writes no row at or past out_rows (and counts such rows in
+    # oob_count), whatever the device cu_seq_lens says.
+    out_rows = min(out_key.shape[0], out_value.shape[0])
     _lib.call("kvc_gather_kv",
               key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
               block_table.stride(0), block_table.shape[1], cu_seq_lens.data_ptr(),
               _ptr(seq_starts), batch, int(max_seq_len), h, d, bs, nb,
               key_cache.element_size(), key_cache.stride(0), key_cache.stride(1),
-              out_key.data_ptr(), out_value.data_ptr(), out_key.stride(0),
+              out_key.data_ptr(), out_value.data_ptr(), out_key.stride(0), out_rows,
               _oob_ptr(oob_count), _stream_handle(dev, stream))
     return out_key, out_value
 
@@ -261,7 +264,8 @@ def copy_page_indices(block_table: torch.Tensor, indptr: torch.Tensor,
                       stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
     """``indices[indptr[r]:indptr[r+1]] = block_table[seq_ids[r], :n_r]``
     (the reference's row index_select + _copy_page_indices_kernel,
-    moe_engine.py:1937-1946)."""
+    moe_engine.py:1937-1946).  ``indices`` must be contiguous; entries past
+    its end are not written."""
     dev = _check_cuda(block_table, indptr, indices, seq_ids)
     if block_table.dtype != torch.int32 or block_table.stride(1) != 1:
         _fail("block_table must be int32 with contiguous rows")
@@ -269,10 +273,13 @@ def copy_page_indices(block_table: torch.Tensor, indptr: torch.Tensor,
         _fail("indptr and indices must be int32")
     if seq_ids is not None and seq_ids.dtype != torch.int32:
         _fail("seq_ids must be int32")
+    if not indices.is_contiguous():
+        _fail("indices must be contiguous")
     num_reqs = indptr.numel() - 1
     _lib.call("kvc_copy_page_indices", block_table.data_ptr(), block_table.stride(0),
               block_table.shape[0], _ptr(seq_ids), indptr.data_ptr(), num_reqs,
-              block_table.shape[1], indices.data_ptr(), _stream_handle(dev, stream))
+              block_table.shape[1], indices.data_ptr(), indices.numel(),
+              _stream_handle(dev, stream))
     return indices
 
 

@@ -79,7 +79,9 @@ int kvc_reshape_and_cache_flash(
  * it are not written).  block_table_width is the number of entries per
  * block-table row.  Rows whose position falls outside the row or whose entry is
  * outside [0, num_blocks) are zero-filled and counted in *oob_count when
- * non-null.
+ * non-null.  out_rows is the number of rows out_key and out_value hold: output
+ * rows outside [0, out_rows) (a cu_seq_lens larger than the outputs) are not
+ * written and are counted in *oob_count.
  * ---------------------------------------------------------------------- */
 int kvc_gather_kv(
     const void* key_cache, const void* value_cache,
@@ -90,7 +92,7 @@ int kvc_gather_kv(
     int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
     int64_t num_blocks, int32_t elem_bytes,
     int64_t cache_block_stride, int64_t cache_token_stride,
-    void* out_key, void* out_value, int64_t out_token_stride,
+    void* out_key, void* out_value, int64_t out_token_stride, int64_t out_rows,
     int32_t* oob_count, void* stream);
 
 /* ------------------------------------------------------------------------
@@ -369,6 +371,7 @@ int kvc_swap_in(const void* host_src, const int32_t* block_ids, int64_t n,
  * index_select at moe_engine.py:1937-1946: for request r (block-table row
  * seq_ids[r], or r when seq_ids is null)
  *   indices[indptr[r] + j] = block_table[row][j],  j < indptr[r+1]-indptr[r].
+ * Entries at or past indices_capacity (the buffer's length) are not written.
  * ---------------------------------------------------------------------- */
 int kvc_compute_slot_mapping(
     const int32_t* block_table, int64_t block_table_row_stride,
@@ -383,7 +386,7 @@ int kvc_copy_page_indices(const int32_t* block_table,
                           int32_t block_table_rows,
                           const int32_t* seq_ids, const int32_t* indptr,
                           int32_t num_reqs, int32_t max_pages_per_req,
-                          int32_t* indices, void* stream);
+                          int32_t* indices, int64_t indices_capacity, void* stream);
 
 #ifdef __cplusplus
 }

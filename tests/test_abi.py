@@ -170,6 +170,40 @@ def test_decode_plan_is_host_only_and_balanced(lib):
     _check_plan_image(indptr, sched, img, lpl)
 
 
+@pytest.mark.parametrize("lens", [[0, 5], [10, 10, 10, 10, 0], [0, 0]])
+def test_decode_plan_empty_requests_without_splits(lib, lens):
+    """Empty requests next to requests of one piece each: no partials exist
+    (max_partitions 1, workspace 0); the run's merge launch then only zeroes
+    the empty requests and must not read partials."""
+    indptr, sched, img, lpl = _plan(lib, lens)
+    assert sched.max_partitions == 1
+    assert sched.num_empty == lens.count(0)
+    assert sched.workspace_bytes == 0
+    assert lib.kvc_decode_workspace_bytes(len(lens), 32, 128, 1) == 0
+    if sum(lens) == 0:
+        assert sched.num_segments == 0 and sched.num_pieces == 0
+    else:
+        _check_plan_image(indptr, sched, img, lpl)
+        rec = img[sched.pieces_offset:sched.pieces_offset + 8 * sched.num_pieces].reshape(-1, 8)
+        assert (rec[:, 3] == -1).all()          # every piece is written directly
+    nparts = img[sched.nparts_offset:sched.nparts_offset + sched.batch]
+    assert nparts.tolist() == [0 if ln == 0 else 1 for ln in lens]
+
+
+def test_decode_run_refuses_split_plan_without_partials(lib):
+    """A plan that splits a request needs the partials workspace: the run is
+    refused on the host (no launch) when it is absent or too small."""
+    indptr, sched, img, lpl = _plan(lib, [0, 1000, 3], hint=8)
+    assert sched.max_partitions > 1 and sched.workspace_bytes > 0
+    fake = 1 << 20     # aligned, never dereferenced: the call fails before any launch
+    for ws, nbytes in ((None, 0), (fake, sched.workspace_bytes - 256)):
+        st = lib.kvc_batch_decode_run(ctypes.byref(sched), fake, fake, 4096, fake, fake,
+                                      2 * 16 * 1024, 1024, 100, fake, fake, 100, fake,
+                                      0.088, ws, nbytes, fake, 4096, None, None)
+        assert st == 4, lib.kvc_last_error()
+        assert b"workspace" in lib.kvc_last_error()
+
+
 def test_decode_plan_random_batches(lib):
     rng = np.random.default_rng(0)
     for trial in range(30):
@@ -226,7 +260,12 @@ def test_entry_points_validate_before_touching_the_gpu(lib):
     assert lib.kvc_swap_out(None, None, 65536, 65536, 8, None, -1, None, 0, None, None, None) == 1
     assert lib.kvc_compute_slot_mapping(None, 0, 1, 1, None, None, None, 0, 0, 0, 16,
                                         None, None, None) == 0
-    assert lib.kvc_copy_page_indices(None, 0, 1, None, None, 0, 1, None, None) == 0
+    assert lib.kvc_copy_page_indices(None, 0, 1, None, None, 0, 1, None, 0, None) == 0
+    assert lib.kvc_copy_page_indices(None, 0, 1, None, None, 0, 1, None, -1, None) == 1
+    assert lib.kvc_gather_kv(None, None, None, 0, 1, None, None, 0, 0, 8, 128, 16, 4, 2,
+                             16384, 1024, None, None, 1024, 0, None, None) == 0
+    assert lib.kvc_gather_kv(None, None, None, 0, 1, None, None, 1, 5, 8, 128, 16, 4, 2,
+                             16384, 1024, None, None, 1024, -1, None, None) == 1
     assert lib.kvc_merge_attention_states(None, None, None, None, 0, 128, None, None, None) == 0
 
 

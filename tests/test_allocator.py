@@ -100,6 +100,22 @@ def test_gpu_only_operations_raise_on_a_cpu_cache():
         c.slot_mapping([0], [1])
 
 
+def test_planning_rejects_bad_seq_ids_and_oversized_sequences():
+    """The host checks every planning call makes before it stages page
+    indices: ids distinct rows of the table (a negative id would wrap in numpy
+    indexing, a repeated one would size the page list past its device buffer),
+    and no sequence longer than its block-table row."""
+    c = cpu_cache(max_seqs=3, max_seq_len=64)
+    for bad in ([-1], [3], [0, 0], [1, 2, 1]):
+        with pytest.raises(ValueError, match="distinct"):
+            c._check_seq_ids(bad)
+    assert c._check_seq_ids([2, 0]).tolist() == [2, 0]
+    assert c._check_seq_ids([]).tolist() == []
+    c._check_page_counts(np.array([4, 0]))        # 64 tokens fill a row exactly
+    with pytest.raises(RuntimeError, match="max_seq_len"):
+        c._check_page_counts(np.array([1, 5]))
+
+
 def test_scheduler_style_workload_keeps_pages_within_budget():
     """A continuous-batching loop in the scheduler's style (ensure_pages per
     decode token, free on completion, LIFO preemption when the pool is short):

@@ -146,6 +146,28 @@ def test_decode_empty_request_gives_zero_and_neg_inf_lse(gpu):
         assert_attn_close(out.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("lens", [[0, 5], [10, 10, 10, 10, 0], [0, 0]])
+def test_decode_empty_requests_when_no_request_is_split(gpu, lens):
+    """Regression: empty requests beside requests of one piece each (the plan
+    has max_partitions 1 and no partials workspace).  The merge launch zeroes
+    the empty requests without reading partials; the rest match the oracle."""
+    print(f"decode empty-request batch {lens}", flush=True)
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, 8, 128, 24)
+    q = randn_bf16((len(lens), 32, 128), 25, device=gpu)
+    (out, lse), w = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, 32, 8, 128)
+    assert w.schedule.max_partitions == 1 and w.schedule.workspace_bytes == 0
+    assert w.schedule.num_empty == lens.count(0)
+    ref, ref_lse = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
+    for b, ln in enumerate(lens):
+        if ln == 0:
+            assert int(out[b].abs().sum()) == 0
+            assert torch.isneginf(lse[b]).all()
+    assert_attn_close(out.float().cpu().numpy(), ref)
+    live = [b for b, ln in enumerate(lens) if ln]
+    if live:
+        assert np.allclose(lse[live].cpu().numpy(), ref_lse[live], atol=1e-3, rtol=1e-4)
+
+
 def test_decode_q_view_and_out_buffer(gpu):
     # q as q_buf[:B] of a larger static buffer, out written into a view of a
     # larger [N, Hq*D] buffer (the engine's attn_out_buf), combined KV tensor.

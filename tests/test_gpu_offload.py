@@ -1,7 +1,10 @@
 """GPU tests of the host-memory KV policies: layer-wise offload through two
 scratchpads and three streams gives bit-identical attention to the all-
-resident layout and writes the new prefill blocks back exactly; swap-based
-preemption resumes a request with bit-identical decode outputs."""
+resident layout, within the attention tolerance of the oracle's x-packed
+decode over the history plus the appended token, and writes the new prefill
+blocks back exactly; swap-based preemption resumes a request with
+bit-identical decode outputs, within the tolerance of the oracle's decode
+over a CPU model of every request's rows."""
 import numpy as np
 import pytest
 import torch
@@ -9,6 +12,8 @@ import torch
 from gpu_offloading_amd import ops, workloads
 from gpu_offloading_amd.kv_cache import PagedKVCache
 from gpu_offloading_amd.offload import KVOffloadPipeline, PagedOffloadKV, SwapPreemption
+from helpers import assert_attn_close, oracle_decode_rows, u16
+from oracle import kv_oracle as orc
 
 pytestmark = pytest.mark.gpu
 
@@ -41,20 +46,48 @@ def _step(kv, pipe, ks, vs, qs):
     return [o.clone() for o in outs]
 
 
+def _oracle_offload_decode(hist_k, hist_v, new_k, new_v, q, scale):
+    """The oracle's x-packed decode (orc.paged_attention_xpacked, fp16) of
+    every decode sequence over its history rows plus this step's new row,
+    laid out in consecutive blocks of a scratch cache; all inputs uint16
+    bits."""
+    H, D, x = q.shape[1], q.shape[2], 8
+    lens = [len(h) + 1 for h in hist_k]
+    nblk = [(n + 15) // 16 for n in lens]
+    kc = np.zeros((sum(nblk), H, D // x, 16, x), np.uint16)
+    vc = np.zeros((sum(nblk), H, D, 16), np.uint16)
+    bt = np.zeros((len(lens), max(nblk)), np.int32)
+    start = 0
+    for i, n in enumerate(lens):
+        bt[i, :nblk[i]] = np.arange(start, start + nblk[i])
+        orc.reshape_and_cache_xpacked(np.concatenate([hist_k[i], new_k[i:i + 1]]),
+                                      np.concatenate([hist_v[i], new_v[i:i + 1]]), kc, vc,
+                                      start * 16 + np.arange(n))
+        start += nblk[i]
+    out, *_ = orc.paged_attention_xpacked(q, kc, vc, bt, np.array(lens), scale, "fp16")
+    return out
+
+
 @pytest.mark.parametrize("ratio,mode", [(0.5, "random"), (0.9, "contiguous")])
 def test_offload_pipeline_matches_resident_layout(gpu, ratio, mode):
+    """Bit-identical to the all-resident layout, and within the attention
+    tolerance of the oracle's x-packed decode over each decode sequence's
+    history plus the step's appended token."""
     dec, pre, L, H = [100, 37, 300, 64, 1], [40, 17], 5, 4
     off = PagedOffloadKV(dec, pre, L, H, 128, ratio, device=gpu, allocation_mode=mode, seed=3)
     res = PagedOffloadKV(dec, pre, L, H, 128, 0.0, device=gpu, allocation_mode="random", seed=4)
     assert off.decode_offload_blocks > 0 and off.prefill_offload_blocks > 0
     g = torch.Generator(device=gpu).manual_seed(70)
+    hist = {}                      # (layer, decode index) -> (K bits, V bits)
     for layer in range(L):
         for i, n in enumerate(dec):
             k = torch.randn(n, H, 128, generator=g, device=gpu).half()
             v = torch.randn(n, H, 128, generator=g, device=gpu).half()
             off.load_history(layer, i, k, v)
             res.load_history(layer, i, k, v)
+            hist[layer, i] = (u16(k), u16(v))
     pipe = KVOffloadPipeline(off)
+    P = off.num_prefill_tokens
     for step in range(2):   # the second step reuses both scratchpads
         T = off.total_tokens
         ks = [torch.randn(T, H, 128, generator=g, device=gpu).half() for _ in range(L)]
@@ -64,6 +97,11 @@ def test_offload_pipeline_matches_resident_layout(gpu, ratio, mode):
         want = _step(res, None, ks, vs, qs)
         for layer in range(L):
             assert torch.equal(got[layer], want[layer]), (step, layer)
+            ref = _oracle_offload_decode([hist[layer, i][0] for i in range(len(dec))],
+                                         [hist[layer, i][1] for i in range(len(dec))],
+                                         u16(ks[layer][P:]), u16(vs[layer][P:]),
+                                         u16(qs[layer]), 0.0884)
+            assert_attn_close(got[layer].float().cpu().numpy(), ref)
         # the prefill sequences' offloaded blocks went back to host memory
         for layer in range(1, L):
             for b in range(len(pre)):
@@ -89,6 +127,8 @@ def test_swap_preemption_resumes_bit_identically(gpu):
                          free_page_order=workloads.randperm(400, 72), **kw)
     g = torch.Generator(device=gpu).manual_seed(73)
     lens = [300, 450, 500, 420]
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    rows = {}                      # (request, layer) -> [K bits, V bits] of its rows so far
     for cache in (tight, ample):
         g2 = torch.Generator(device=gpu).manual_seed(74)
         for s, n in enumerate(lens):
@@ -98,6 +138,9 @@ def test_swap_preemption_resumes_bit_identically(gpu):
             k = torch.randn(sum(lens), Hkv, 128, generator=g2, device=gpu).to(torch.bfloat16)
             v = torch.randn(sum(lens), Hkv, 128, generator=g2, device=gpu).to(torch.bfloat16)
             cache.append(layer, k, v, slots)
+            if cache is tight:
+                for r in range(4):
+                    rows[r, layer] = [u16(k[cu[r]:cu[r + 1]]), u16(v[cu[r]:cu[r + 1]])]
         cache.advance(range(4), lens)
     pre = SwapPreemption(tight)
     where = {0: 0, 1: 1, 2: 2, 3: 3}   # request -> slot in the tight cache
@@ -133,4 +176,14 @@ def test_swap_preemption_resumes_bit_identically(gpu):
             outs[name] = res
         for layer in range(L):
             assert torch.equal(outs["tight"][layer], outs["ample"][layer]), (step, layer)
+            for j, r in enumerate(active):
+                rows[r, layer][0] = np.concatenate([rows[r, layer][0], u16(k[layer][j:j + 1])])
+                rows[r, layer][1] = np.concatenate([rows[r, layer][1], u16(v[layer][j:j + 1])])
+            # oracle: the resumed request from its resume on, every request at the end
+            check = [j for j, r in enumerate(active) if (r == 3 and step >= 5) or step == 7]
+            if check:
+                ref, _ = oracle_decode_rows(u16(q[layer][check]),
+                                            [rows[active[j], layer][0] for j in check],
+                                            [rows[active[j], layer][1] for j in check])
+                assert_attn_close(outs["tight"][layer][check].float().cpu().numpy(), ref)
     assert pre.swaps_out == 1 and pre.swaps_in == 1 and not pre.is_swapped(3)
