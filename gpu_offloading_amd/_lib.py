@@ -99,6 +99,9 @@ SIGNATURES = {
     "kvc_batch_decode_run": (c_int, [
         POINTER(KvcDecodeSchedule), _I32P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64,
         _I32P, _I32P, c_int64, _I32P, c_float, _P, c_int64, _P, c_int64, _P, _P]),
+    "kvc_batch_decode_run_noalloc": (c_int, [
+        POINTER(KvcDecodeSchedule), _I32P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64,
+        _I32P, _I32P, c_int64, _I32P, c_float, _P, c_int64, _P, _P]),
     "kvc_batch_decode_append_run": (c_int, [
         POINTER(KvcDecodeSchedule), _I32P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64,
         _I32P, _I32P, c_int64, _I32P, _P, c_int64, _P, c_int64, c_float, _P, c_int64, _P,

@@ -53,6 +53,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 namespace kvc {
 namespace {
@@ -1202,6 +1203,76 @@ extern "C" int kvc_batch_decode_run(
   return decode_run(sched, plan, q, q_batch_stride, key_cache, value_cache, cache_block_stride,
                     cache_token_stride, num_blocks, indptr, indices, num_indices, last_page_len,
                     nullptr, 0, nullptr, 0, sm_scale, workspace, workspace_bytes, out,
+                    out_batch_stride, lse, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode run: the split-K partials live in this library's own
+// device array instead of a caller workspace.  Each GPU the library runs on
+// holds one copy of the array until the process ends; all calls on one GPU
+// share it (calls that overlap on one GPU race on it).  The partials are
+// written before they are read within a call, so nothing needs clearing.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) char scratch[KVC_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on `device`, which must be the current device:
+// looked up once per device (hipGetSymbolAddress; the array's host-side name
+// is not a device address and is never passed to a kernel or a copy).
+int scratch_address(int device, void** out) {
+  KVC_REQUIRE(device >= 0 && device < kMaxDevices, KVC_ERR_INVALID_ARG,
+              "device ordinal out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    KVC_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    KVC_REQUIRE(p != nullptr, KVC_ERR_HIP, "hipGetSymbolAddress gave a null address");
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return ok();
+}
+
+}  // namespace
+
+extern "C" int kvc_batch_decode_run_noalloc(
+    const kvc_decode_schedule* sched, const int32_t* plan, const void* q,
+    int64_t q_batch_stride, const void* key_cache, const void* value_cache,
+    int64_t cache_block_stride, int64_t cache_token_stride, int64_t num_blocks,
+    const int32_t* indptr, const int32_t* indices, int64_t num_indices,
+    const int32_t* last_page_len, float sm_scale, void* out, int64_t out_batch_stride,
+    float* lse, void* stream) {
+  KVC_REQUIRE(sched, KVC_ERR_INVALID_ARG, "null schedule");
+  if (sched->batch == 0) return ok();
+  const int64_t need =
+      kvc_decode_workspace_bytes(sched->batch, sched->num_qo_heads, sched->head_dim,
+                                 sched->max_partitions);
+  KVC_REQUIRE(need <= KVC_NOALLOC_SCRATCH_BYTES, KVC_ERR_WORKSPACE,
+              "the batch needs " + std::to_string(need) +
+                  " bytes of split-K partials; the allocation-free run holds at most " +
+                  std::to_string(int64_t(KVC_NOALLOC_SCRATCH_BYTES)) +
+                  " (use kvc_batch_decode_run with a workspace)");
+  int device = -1;
+  KVC_HIP_CHECK(hipGetDevice(&device));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (s) {
+    hipDevice_t sdev = -1;
+    KVC_HIP_CHECK(hipStreamGetDevice(s, &sdev));
+    KVC_REQUIRE(int(sdev) == device, KVC_ERR_INVALID_ARG,
+                "the stream belongs to device " + std::to_string(int(sdev)) +
+                    ", the current device is " + std::to_string(device));
+  }
+  void* ws = nullptr;
+  const int st = scratch_address(device, &ws);
+  if (st != KVC_OK) return st;
+  return decode_run(sched, plan, q, q_batch_stride, key_cache, value_cache, cache_block_stride,
+                    cache_token_stride, num_blocks, indptr, indices, num_indices, last_page_len,
+                    nullptr, 0, nullptr, 0, sm_scale, ws, KVC_NOALLOC_SCRATCH_BYTES, out,
                     out_batch_stride, lse, stream);
 }
 

@@ -170,6 +170,30 @@ int kvc_batch_decode_run(
     void* workspace, int64_t workspace_bytes,
     void* out, int64_t out_batch_stride, float* lse, void* stream);
 
+/* Allocation-free decode run.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation).  Same arguments and
+ * results as kvc_batch_decode_run without the workspace: the split-K
+ * partials live in a device array of the library (KVC_NOALLOC_SCRATCH_BYTES
+ * bytes, one per GPU, held until the process ends).  The call allocates
+ * nothing.  A schedule whose workspace_bytes exceed the array is refused with
+ * KVC_ERR_WORKSPACE.  The stream must belong to the current device (its first
+ * call on a device looks up that device's copy of the array).  All calls on
+ * one GPU share the array: calls that overlap on one GPU (other streams,
+ * other threads) race on it, so serialize them. */
+#define KVC_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+
+int kvc_batch_decode_run_noalloc(
+    const kvc_decode_schedule* schedule, const int32_t* plan,
+    const void* q, int64_t q_batch_stride,
+    const void* key_cache, const void* value_cache,
+    int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t num_blocks,
+    const int32_t* indptr, const int32_t* indices, int64_t num_indices,
+    const int32_t* last_page_len,
+    float sm_scale,
+    void* out, int64_t out_batch_stride, float* lse, void* stream);
+
 /* Fused append + decode for a pure-decode step.  No single counterpart in
  * the reference: it does, in one launch, what the engine does with
  * reshape_and_cache_flash of the step's tokens (moe_engine.py:2344-2347)

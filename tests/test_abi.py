@@ -204,6 +204,23 @@ def test_decode_run_refuses_split_plan_without_partials(lib):
         assert b"workspace" in lib.kvc_last_error()
 
 
+def test_noalloc_run_refuses_partials_beyond_its_array_on_the_host(lib):
+    """kvc_batch_decode_run_noalloc checks the schedule's partials against
+    its fixed device array before touching the GPU (no device here)."""
+    indptr, sched, img, lpl = _plan(lib, [320] * 64, hint=1280)
+    assert sched.workspace_bytes > 16 << 20
+    fake = 1 << 20
+    st = lib.kvc_batch_decode_run_noalloc(ctypes.byref(sched), fake, fake, 4096, fake, fake,
+                                          2 * 16 * 1024, 1024, 2000, fake, fake, 1280, fake,
+                                          0.088, fake, 4096, None, None)
+    assert st == 4
+    assert b"allocation-free" in lib.kvc_last_error()
+    empty = _lib.KvcDecodeSchedule()            # batch 0: nothing to do
+    assert lib.kvc_batch_decode_run_noalloc(ctypes.byref(empty), None, None, 0, None, None,
+                                            0, 0, 0, None, None, 0, None, 0.1, None, 0,
+                                            None, None) == 0
+
+
 def test_decode_plan_random_batches(lib):
     rng = np.random.default_rng(0)
     for trial in range(30):
