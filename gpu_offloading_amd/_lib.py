@@ -52,7 +52,7 @@ class KvcDecodeSchedule(ctypes.Structure):
         ("plan_ints", c_int64),
         ("workspace_bytes", c_int64),
         ("append_pieces", c_int32),
-        ("reserved", c_int32),
+        ("small_batch", c_int32),
     ]
 
 

@@ -526,6 +526,252 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// head_dim 128, small batches: one workgroup per (request, KV head), its
+// kSmallWaves waves splitting the request's pages (wave w takes pages w,
+// w + kSmallWaves, ...), the waves' softmax states merged in LDS.  One launch,
+// no partials in memory and no merge kernel: for batches whose requests fit
+// in kSmallMaxPages pages but would otherwise be cut into one-page segments
+// and merged (batch 1 at a 128-token context: 9 pages).  The plan image holds
+// one segment and one piece per request (empty requests included), so the
+// request's record sits at piece index b.
+// ---------------------------------------------------------------------------
+constexpr int kSmallWaves = 8;
+constexpr int kSmallMaxPages = 2 * kSmallWaves;
+
+template <int G>
+__global__ __launch_bounds__(64 * kSmallWaves) void decode_small_kernel(DecodeArgs a) {
+  using C = LdsCfg<G>;
+  using Tile = BlockTile<1>;
+  constexpr int D = 128;
+  constexpr int kPagesPerWave = kSmallMaxPages / kSmallWaves;
+  __shared__ Tile s_tile[kSmallWaves];
+  __shared__ float s_p[kSmallWaves][kPage * 8];
+  __shared__ float s_m[kSmallWaves][G];
+  __shared__ float s_l[kSmallWaves][G];
+  __shared__ float s_o[kSmallWaves][G][D];
+
+  const int b = blockIdx.x;
+  const int h = blockIdx.y;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int4 desc = a.pieces[2 * b];        // (request, first slot, end slot, -1)
+  const int4 tail = a.pieces[2 * b + 1];    // (request's last slot, its tokens, 0, 0)
+  const int first = desc.y;
+  const int npages = min(desc.z - desc.y, kSmallMaxPages);
+  const int last_len = min(max(tail.y, 0), kPage);
+  Tile& tile = s_tile[wave];
+  float* p_buf = s_p[wave];
+
+  const int t = lane & 15;
+  const int row = lane >> 4;
+  const int gq = row % C::GP;
+  const int split = row / C::GP;
+  // Staging: chunk u of this lane is chunk 64 u + lane of the (16 tokens x
+  // 256 B) image of head h in a page: token (64 u + lane) / 16, chunk lane % 16.
+  const int cc = lane & 15;
+  const uint32_t ts_bytes = uint32_t(a.token_stride * 2);
+  uint32_t st_goff[4];
+  int st_tok[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    st_tok[u] = (64 * u + lane) >> 4;
+    st_goff[u] = uint32_t(st_tok[u]) * ts_bytes + uint32_t(h * D * 2 + cc * 16);
+  }
+  const char* kbytes = reinterpret_cast<const char*>(a.k_cache);
+  const char* vbytes = reinterpret_cast<const char*>(a.v_cache);
+  const int64_t block_bytes = a.block_stride * 2;
+
+  // This wave's pages, their ids and their loads, all issued up front.
+  struct Stage {
+    uint4 k[4], v[4];
+  };
+  Stage st[kPagesPerWave];
+  int32_t ids[kPagesPerWave];
+#pragma unroll
+  for (int i = 0; i < kPagesPerWave; ++i) {
+    const int j = wave + kSmallWaves * i;
+    ids[i] = -1;
+    if (j < npages) {
+      const int64_t slot = int64_t(first) + j;
+      ids[i] = slot < a.num_indices ? a.indices[slot] : -1;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kPagesPerWave; ++i) {
+    const int32_t id = (ids[i] >= 0 && ids[i] < a.num_blocks) ? ids[i] : 0;
+    const char* kb = kbytes + int64_t(id) * block_bytes;
+    const char* vb = vbytes + int64_t(id) * block_bytes;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      st[i].k[u] = make_uint4(0, 0, 0, 0);
+      st[i].v[u] = make_uint4(0, 0, 0, 0);
+    }
+    if (wave + kSmallWaves * i < npages) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        st[i].k[u] = load_stream(kb + st_goff[u]);
+        st[i].v[u] = load_stream(vb + st_goff[u]);
+      }
+    }
+  }
+  // Fused append: lane chunk cc of head h of the request's new K / V row.
+  const bool appending = a.new_k != nullptr && npages > 0 && last_len > 0;
+  uint4 nk = make_uint4(0, 0, 0, 0), nv = make_uint4(0, 0, 0, 0);
+  if (appending) {
+    nk = reinterpret_cast<const uint4*>(a.new_k + int64_t(b) * a.new_k_stride + h * D)[cc];
+    nv = reinterpret_cast<const uint4*>(a.new_v + int64_t(b) * a.new_v_stride + h * D)[cc];
+  }
+
+  uint32_t qw[C::QL][C::CH * 4];
+#pragma unroll
+  for (int ql = 0; ql < C::QL; ++ql) {
+    const uint4* qp = reinterpret_cast<const uint4*>(
+        a.q + int64_t(b) * a.q_stride + int64_t(h * G + gq + 4 * ql) * D + split * C::CH * 8);
+#pragma unroll
+    for (int i = 0; i < C::CH; ++i) {
+      const uint4 x = qp[i];
+      qw[ql][4 * i + 0] = x.x;
+      qw[ql][4 * i + 1] = x.y;
+      qw[ql][4 * i + 2] = x.z;
+      qw[ql][4 * i + 3] = x.w;
+    }
+  }
+  float m_run[C::QL], l_run[C::QL], acc[G][2];
+#pragma unroll
+  for (int ql = 0; ql < C::QL; ++ql) {
+    m_run[ql] = kNegBig;
+    l_run[ql] = 0.f;
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
+
+#pragma unroll
+  for (int i = 0; i < kPagesPerWave; ++i) {
+    const int j = wave + kSmallWaves * i;
+    if (j >= npages) break;  // uniform over the wave
+    const int slot = first + j;
+    const int32_t id = ids[i];
+    const bool ok = id >= 0 && id < a.num_blocks;
+    const int valid = !ok ? 0 : (slot == tail.x ? last_len : kPage);
+    Stage& r = st[i];
+    if (appending && slot == tail.x && ok) {
+      // The request's last page: its new token row (row valid - 1) comes
+      // from the step's rows and is written to the cache.
+      char* kdst = const_cast<char*>(kbytes) + int64_t(id) * block_bytes;
+      char* vdst = const_cast<char*>(vbytes) + int64_t(id) * block_bytes;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (st_tok[u] == valid - 1) {
+          r.k[u] = nk;
+          r.v[u] = nv;
+          store_stream(kdst + st_goff[u], nk);
+          store_stream(vdst + st_goff[u], nv);
+        }
+      }
+    }
+    // Stage the page into this wave's tile (rows past `valid` as zeros).
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool live = st_tok[u] < valid;
+      tile.k[st_tok[u] * Tile::kRowChunks + cc] = live ? r.k[u] : make_uint4(0, 0, 0, 0);
+      tile.v[st_tok[u] * Tile::kRowChunks + cc] = live ? r.v[u] : make_uint4(0, 0, 0, 0);
+    }
+    wave_lds_fence();
+    // q.k: lane (t, gq) over its chunks of K row t.
+    float dots[C::QL];
+#pragma unroll
+    for (int ql = 0; ql < C::QL; ++ql) dots[ql] = 0.f;
+    const uint4* krow = tile.k + t * Tile::kRowChunks + split * C::CH;
+#pragma unroll
+    for (int c = 0; c < C::CH; ++c) {
+      const uint4 kv = krow[c];
+#pragma unroll
+      for (int ql = 0; ql < C::QL; ++ql) {
+        dots[ql] = dot2_bf16(qw[ql][4 * c + 0], kv.x, dots[ql]);
+        dots[ql] = dot2_bf16(qw[ql][4 * c + 1], kv.y, dots[ql]);
+        dots[ql] = dot2_bf16(qw[ql][4 * c + 2], kv.z, dots[ql]);
+        dots[ql] = dot2_bf16(qw[ql][4 * c + 3], kv.w, dots[ql]);
+      }
+    }
+#pragma unroll
+    for (int off = 16 * C::GP; off < 64; off <<= 1)
+#pragma unroll
+      for (int ql = 0; ql < C::QL; ++ql) dots[ql] += __shfl_xor(dots[ql], off);
+    const bool live = t < valid;
+    float alpha[C::QL];
+#pragma unroll
+    for (int ql = 0; ql < C::QL; ++ql) {
+      const float s = live ? dots[ql] * a.scale_log2 : kNegBig;
+      const float m_new = fmaxf(m_run[ql], row16_max(s));
+      const float p = live ? fast_exp2(s - m_new) : 0.f;
+      alpha[ql] = fast_exp2(m_run[ql] - m_new);
+      l_run[ql] = fmaf(l_run[ql], alpha[ql], row16_sum(p));
+      m_run[ql] = m_new;
+      if (row < C::GP) p_buf[t * G + gq + 4 * ql] = p;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float al = readlane_f(alpha[g / 4], 16 * (g % 4));
+      acc[g][0] *= al;
+      acc[g][1] *= al;
+    }
+    wave_lds_fence();
+    // p.v over the page's 16 rows (rows past `valid` are zero).
+    const uint32_t* vcol = reinterpret_cast<const uint32_t*>(tile.v) + lane;
+#pragma unroll
+    for (int tt = 0; tt < kPage; ++tt) {
+      const uint32_t vw = vcol[tt * Tile::kRowChunks * 4];
+      const float v0 = bf16lo(vw);
+      const float v1 = bf16hi(vw);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pg = p_buf[tt * G + g];
+        acc[g][0] = fmaf(pg, v0, acc[g][0]);
+        acc[g][1] = fmaf(pg, v1, acc[g][1]);
+      }
+    }
+    wave_lds_fence();  // the tile and p_buf are rewritten by the next page
+  }
+
+  // The waves' states (log2 domain) into LDS, then one merged output row per
+  // query head; lanes cover (query head, dim).
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float l = readlane_f(l_run[g / 4], 16 * (g % 4));
+    const float m = readlane_f(m_run[g / 4], 16 * (g % 4));
+    if (lane == 0) {
+      s_m[wave][g] = m;
+      s_l[wave][g] = l;
+    }
+    s_o[wave][g][2 * lane] = acc[g][0];
+    s_o[wave][g][2 * lane + 1] = acc[g][1];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < G * D; e += 64 * kSmallWaves) {
+    const int g = e / D;
+    const int d = e - g * D;
+    float mx = kNegBig;
+#pragma unroll
+    for (int w = 0; w < kSmallWaves; ++w)
+      if (s_l[w][g] > 0.f) mx = fmaxf(mx, s_m[w][g]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSmallWaves; ++w) {
+      if (s_l[w][g] > 0.f) {
+        const float wt = fast_exp2(s_m[w][g] - mx);
+        L = fmaf(s_l[w][g], wt, L);
+        O = fmaf(s_o[w][g][d], wt, O);
+      }
+    }
+    const int hq = h * G + g;
+    a.out[int64_t(b) * a.out_stride + int64_t(hq) * D + d] = f32_to_bf16(L > 0.f ? O / L : 0.f);
+    if (a.lse && d == 0)
+      a.lse[int64_t(b) * a.num_kv_heads * G + hq] =
+          L > 0.f ? (mx + fast_log2(L)) * kLn2 : -INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // head_dim 64 / 256: register kernel.
 // ---------------------------------------------------------------------------
 // Load the D/16 bf16 elements one lane owns (D/32 32-bit words).
@@ -986,6 +1232,68 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, const int32_t* last_p
     segs = std::min<int64_t>(segs, total);
   }
   KVC_REQUIRE(segs <= (int64_t(1) << 30), KVC_ERR_INVALID_ARG, "too many segments");
+
+  // Small batches (head_dim 128, no forced segment count): when every request
+  // fits in kSmallMaxPages pages and the equal segments would cut a request,
+  // one workgroup per (request, KV head) streams it and merges its waves'
+  // states in LDS instead (no partials, no merge launch).
+  int64_t max_pages = 0;
+  for (int b = 0; b < batch; ++b)
+    max_pages = std::max<int64_t>(max_pages, indptr_host[b + 1] - indptr_host[b]);
+  bool splits = false;
+  for (int64_t s = 1, bb = 0; s < segs && !splits; ++s) {
+    const int64_t g = s * total / segs;  // first page of segment s
+    while (bb < batch && indptr_host[bb + 1] <= g) ++bb;
+    splits = bb < batch && indptr_host[bb] < g;  // pages g-1 and g in request bb
+  }
+  if (num_segments_hint <= 0 && head_dim == 128 && total > 0 && max_pages <= kSmallMaxPages &&
+      splits) {
+    const int64_t need = kvc_decode_plan_ints(batch, batch);
+    sched->batch = batch;
+    sched->num_qo_heads = num_qo_heads;
+    sched->num_kv_heads = num_kv_heads;
+    sched->head_dim = head_dim;
+    sched->page_size = page_size;
+    sched->num_segments = batch;
+    sched->num_head_groups = num_kv_heads;
+    sched->heads_per_group = 1;
+    sched->total_pages = int32_t(total);
+    sched->num_empty = num_empty;
+    sched->plan_ints = need;
+    sched->small_batch = 1;
+    KVC_REQUIRE(plan_host && plan_capacity >= need, KVC_ERR_WORKSPACE,
+                "plan buffer too small: need " + std::to_string(need) + " int32");
+    // One segment and one piece per request, empty requests included.
+    int32_t* segments = plan_host;
+    int32_t* pieces = plan_host + 4 * int64_t(batch);
+    int32_t* nparts = pieces + 8 * (2 * int64_t(batch));
+    for (int b = 0; b < batch; ++b) {
+      const int32_t p0 = indptr_host[b], p1 = indptr_host[b + 1];
+      int32_t* rec = segments + 4 * b;
+      rec[0] = b;
+      rec[1] = b + 1;
+      rec[2] = p0;
+      rec[3] = p1 - p0;
+      int32_t* pc = pieces + 8 * b;
+      pc[0] = b;
+      pc[1] = p0;
+      pc[2] = p1;
+      pc[3] = -1;
+      pc[4] = p1 - 1;
+      pc[5] = last_page_len_host[b];
+      pc[6] = 0;
+      pc[7] = 0;
+      nparts[b] = p1 > p0 ? 1 : 0;
+    }
+    sched->num_pieces = batch;
+    sched->pieces_offset = 4 * batch;
+    sched->nparts_offset = 4 * batch + 16 * batch;
+    sched->max_partitions = 1;
+    sched->workspace_bytes = 0;
+    sched->append_pieces = 1;
+    return ok();
+  }
+
   const int64_t need = kvc_decode_plan_ints(batch, int32_t(segs));
   sched->batch = batch;
   sched->num_qo_heads = num_qo_heads;
@@ -998,6 +1306,7 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, const int32_t* last_p
   sched->total_pages = int32_t(total);
   sched->num_empty = num_empty;
   sched->plan_ints = need;
+  sched->small_batch = 0;
   KVC_REQUIRE(plan_host && plan_capacity >= need, KVC_ERR_WORKSPACE,
               "plan buffer too small: need " + std::to_string(need) + " int32");
 
@@ -1051,7 +1360,6 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, const int32_t* last_p
   sched->workspace_bytes =
       kvc_decode_workspace_bytes(batch, num_qo_heads, head_dim, max_parts);
   sched->append_pieces = append_pieces;
-  sched->reserved = 0;
   return ok();
 }
 
@@ -1075,10 +1383,14 @@ int decode_run(const kvc_decode_schedule* sched, const int32_t* plan, const void
   KVC_REQUIRE(Hkv > 0 && Hq % Hkv == 0, KVC_ERR_INVALID_ARG, "bad head counts");
   const int group = Hq / Hkv;
   KVC_REQUIRE(sched->page_size == kPage, KVC_ERR_UNSUPPORTED, "page_size must be 16");
+  const bool small = sched->small_batch != 0;
   KVC_REQUIRE(sched->num_segments >= 0 && sched->max_partitions >= 1 &&
-                  sched->heads_per_group == heads_per_workgroup(group, D, Hkv) &&
-                  sched->num_head_groups ==
-                      (Hkv + sched->heads_per_group - 1) / sched->heads_per_group &&
+                  (small ? (D == 128 && sched->heads_per_group == 1 &&
+                            sched->num_head_groups == Hkv && sched->num_segments == batch &&
+                            sched->num_pieces == batch && sched->max_partitions == 1)
+                         : (sched->heads_per_group == heads_per_workgroup(group, D, Hkv) &&
+                            sched->num_head_groups ==
+                                (Hkv + sched->heads_per_group - 1) / sched->heads_per_group)) &&
                   sched->plan_ints == kvc_decode_plan_ints(batch, sched->num_segments),
               KVC_ERR_INVALID_ARG, "schedule not produced by kvc_decode_plan");
   KVC_REQUIRE(num_blocks > 0 && num_indices >= sched->total_pages, KVC_ERR_INVALID_ARG,
@@ -1143,11 +1455,13 @@ int decode_run(const kvc_decode_schedule* sched, const int32_t* plan, const void
   a.new_v_stride = new_value_stride;
   if (new_key || new_value) {
     KVC_REQUIRE(new_key && new_value, KVC_ERR_INVALID_ARG, "new_key and new_value go together");
-    KVC_REQUIRE(D == 128 && sched->heads_per_group == 8 && sched->append_pieces <= kNewMax,
+    KVC_REQUIRE(D == 128 &&
+                    (small || (sched->heads_per_group == 8 && sched->append_pieces <= kNewMax)),
                 KVC_ERR_UNSUPPORTED,
-                "fused append needs head_dim 128, a multiple of 8 KV heads with group <= 4, "
-                "and at most " + std::to_string(kNewMax) + " leading pieces per segment "
-                "holding request ends (schedule->append_pieces)");
+                "fused append needs head_dim 128 and either a small-batch schedule or a "
+                "multiple of 8 KV heads with group <= 4 and at most " +
+                    std::to_string(kNewMax) + " leading pieces per segment holding request "
+                    "ends (schedule->append_pieces)");
     KVC_REQUIRE(new_key_stride >= int64_t(Hkv) * D && new_value_stride >= int64_t(Hkv) * D,
                 KVC_ERR_INVALID_ARG, "new row stride smaller than a row");
     KVC_REQUIRE(aligned(new_key, 16) && aligned(new_value, 16) && new_key_stride % 8 == 0 &&
@@ -1155,6 +1469,23 @@ int decode_run(const kvc_decode_schedule* sched, const int32_t* plan, const void
                 KVC_ERR_ALIGNMENT, "new rows must be 16-byte aligned");
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
+
+  if (small) {
+    // One workgroup per (request, KV head); outputs (empty requests too)
+    // are written in the launch, no merge follows.
+    const dim3 grid{unsigned(batch), unsigned(Hkv)};
+    switch (group) {
+      case 1: decode_small_kernel<1><<<grid, 64 * kSmallWaves, 0, s>>>(a); break;
+      case 2: decode_small_kernel<2><<<grid, 64 * kSmallWaves, 0, s>>>(a); break;
+      case 4: decode_small_kernel<4><<<grid, 64 * kSmallWaves, 0, s>>>(a); break;
+      case 8: decode_small_kernel<8><<<grid, 64 * kSmallWaves, 0, s>>>(a); break;
+      default:
+        return set_error(KVC_ERR_UNSUPPORTED, "decode_run: unsupported group size " +
+                                                  std::to_string(group));
+    }
+    KVC_LAUNCH_CHECK();
+    return ok();
+  }
 
   if (sched->num_segments > 0) {
     bool launched = false;

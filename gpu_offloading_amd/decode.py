@@ -263,10 +263,11 @@ class BatchDecodeWithPagedKVCacheWrapper:
     @property
     def fused_append_supported(self) -> bool:
         """Whether ``run_with_append`` can serve the planned batch (head_dim
-        128, 8 KV heads per workgroup, few request ends per segment)."""
+        128 and either a small-batch schedule or 8 KV heads per workgroup
+        with few request ends per segment)."""
         sc = self._sched
-        return (sc is not None and sc.head_dim == 128 and sc.heads_per_group == 8
-                and sc.append_pieces <= 4)
+        return (sc is not None and sc.head_dim == 128
+                and (sc.small_batch == 1 or (sc.heads_per_group == 8 and sc.append_pieces <= 4)))
 
     def run_with_append(self, q: torch.Tensor,
                         paged_kv_cache: Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]],

@@ -142,7 +142,8 @@ typedef struct kvc_decode_schedule {
   int64_t workspace_bytes;  /* bytes kvc_batch_decode_run will use         */
   int32_t append_pieces;    /* most leading pieces of a segment that reach
                                a request end (fused append supports <= 4)  */
-  int32_t reserved;
+  int32_t small_batch;      /* 1: one workgroup per (request, KV head), its
+                               waves splitting the pages (see below)       */
 } kvc_decode_schedule;
 
 int64_t kvc_decode_plan_ints(int32_t batch, int32_t num_segments);

@@ -78,11 +78,33 @@ def _plan(lib, lens, hq=32, hkv=8, d=128, hint=0, cus=256):
     return indptr, sched, img, lpl
 
 
+def _check_small_plan_image(indptr, sched, img, lpl):
+    """Small-batch plans: one segment and one piece per request (empty ones
+    included), piece b = request b's whole page range, no partials."""
+    B = sched.batch
+    assert sched.small_batch == 1 and sched.num_segments == B and sched.num_pieces == B
+    assert sched.heads_per_group == 1 and sched.num_head_groups == sched.num_kv_heads
+    assert sched.max_partitions == 1 and sched.workspace_bytes == 0
+    segs = img[:4 * B].reshape(-1, 4)
+    rec = img[sched.pieces_offset:sched.pieces_offset + 8 * B].reshape(-1, 8)
+    nparts = img[sched.nparts_offset:sched.nparts_offset + B]
+    pages = np.diff(indptr)
+    assert (segs[:, 0] == np.arange(B)).all() and (segs[:, 1] == np.arange(1, B + 1)).all()
+    assert (segs[:, 2] == indptr[:-1]).all() and (segs[:, 3] == pages).all()
+    assert (rec[:, 0] == np.arange(B)).all() and (rec[:, 3] == -1).all()
+    assert (rec[:, 1] == indptr[:-1]).all() and (rec[:, 2] == indptr[1:]).all()
+    assert (rec[:, 4] == indptr[1:] - 1).all() and (rec[:, 5] == lpl).all()
+    assert (nparts == (pages > 0)).all()
+    assert pages.max() <= 16
+
+
 def _check_plan_image(indptr, sched, img, lpl):
     """Segments are contiguous, equal to within one page, at most 128 pages,
     and their pieces tile every request's pages exactly once, numbered
     0..n-1 per request (-1 when a request is a single piece), each carrying
     its request's last slot and last-page length."""
+    if sched.small_batch:
+        return _check_small_plan_image(indptr, sched, img, lpl)
     S = sched.num_segments
     segs = img[:4 * S].reshape(-1, 4)
     rec = img[sched.pieces_offset:sched.pieces_offset + 8 * sched.num_pieces].reshape(-1, 8)
@@ -202,6 +224,26 @@ def test_decode_run_refuses_split_plan_without_partials(lib):
                                       0.088, ws, nbytes, fake, 4096, None, None)
         assert st == 4, lib.kvc_last_error()
         assert b"workspace" in lib.kvc_last_error()
+
+
+def test_small_batch_plans_are_chosen_only_where_segments_would_split(lib):
+    """Per-request workgroups replace the equal segments when every request
+    fits in 16 pages and the segments would cut one (batch 1 at the
+    reference's 128-token context: 9 one-page segments and a merge
+    otherwise); never with a forced segment count or head_dim != 128."""
+    for lens in ([129], [129] * 4, [0, 129, 3], [256] * 40, [1, 2, 200]):
+        indptr, sched, img, lpl = _plan(lib, lens)
+        assert sched.small_batch == 1, lens
+        _check_plan_image(indptr, sched, img, lpl)
+        assert sched.num_empty == lens.count(0)
+    for lens, kw in (([257], {}),                      # 17 pages: too long
+                     ([3000] * 64, {}),                 # the bench's shape
+                     ([16] * 300, {}),                  # one page each: nothing to split
+                     ([129], {"hint": 9}),              # forced segments
+                     ([129], {"d": 64, "hq": 32, "hkv": 8})):
+        indptr, sched, img, lpl = _plan(lib, lens, **kw)
+        assert sched.small_batch == 0, (lens, kw)
+        _check_plan_image(indptr, sched, img, lpl)
 
 
 def test_noalloc_run_refuses_partials_beyond_its_array_on_the_host(lib):

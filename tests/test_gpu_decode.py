@@ -168,6 +168,52 @@ def test_decode_empty_requests_when_no_request_is_split(gpu, lens):
         assert np.allclose(lse[live].cpu().numpy(), ref_lse[live], atol=1e-3, rtol=1e-4)
 
 
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_decode_small_batch_kernel(gpu, group):
+    """Small-batch schedules (one workgroup per request and KV head, the
+    waves' states merged in LDS): against the oracle and fp32 SDPA, empty
+    requests zero / -inf, rows past each request's end poisoned with NaN."""
+    print(f"decode small-batch kernel, group {group}", flush=True)
+    hkv = 8 if group <= 4 else 4
+    hq = hkv * group
+    lens = [129, 1, 0, 256, 17, 16, 100]
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, hkv, 128, 26 + group)
+    for b, ln in enumerate(lens):
+        if ln % 16:
+            last = bt[b, (ln - 1) // 16]
+            kc[last, ln % 16:] = float("nan")
+            vc[last, ln % 16:] = float("nan")
+    q = randn_bf16((len(lens), hq, 128), 27, device=gpu)
+    (out, lse), w = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, hq, hkv, 128)
+    assert w.schedule.small_batch == 1 and w.schedule.workspace_bytes == 0
+    ref, ref_lse = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
+    got = out.float().cpu().numpy()
+    assert_attn_close(got, ref)
+    live = [b for b, ln in enumerate(lens) if ln]
+    kcf, vcf = kc.clone(), vc.clone()
+    kcf[torch.isnan(kcf)] = 0
+    vcf[torch.isnan(vcf)] = 0
+    assert_attn_close(got[live], _sdpa_ref(q[live], kcf, vcf, bt[live], [lens[b] for b in live]))
+    assert np.allclose(lse[live].cpu().numpy(), ref_lse[live], atol=1e-3, rtol=1e-4)
+    assert int(out[2].abs().sum()) == 0 and torch.isneginf(lse[2]).all()
+    # one-token request: exactly V[0] of its KV heads
+    v0 = vc[bt[1, 0], 0]
+    assert torch.equal(out[1].cpu(), v0.repeat_interleave(group, dim=0))
+
+
+def test_decode_batch1_at_the_reference_shape_uses_one_launch(gpu):
+    """The reference's published decode shape (one 129-token request,
+    Mixtral heads) plans a small-batch schedule and matches the oracle."""
+    lens = [129]
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, 8, 128, 28)
+    q = randn_bf16((1, 32, 128), 29, device=gpu)
+    (out, lse), w = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, 32, 8, 128)
+    assert w.schedule.small_batch == 1 and w.schedule.max_partitions == 1
+    ref, ref_lse = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
+    assert_attn_close(out.float().cpu().numpy(), ref)
+    assert np.abs(lse.cpu().numpy() - ref_lse).max() < 1e-3
+
+
 def test_decode_q_view_and_out_buffer(gpu):
     # q as q_buf[:B] of a larger static buffer, out written into a view of a
     # larger [N, Hq*D] buffer (the engine's attn_out_buf), combined KV tensor.

@@ -76,9 +76,23 @@ def test_fused_append_step_order_and_mha(gpu):
     assert _step_both_ways(gpu, lens, 16, 16, 900, 93, order=order)
 
 
+@pytest.mark.parametrize("hkv,hq,lens", [
+    (8, 32, [128]),                     # the reference's batch-1 decode shape
+    (8, 32, [0, 128, 33, 5, 255]),      # empty request, page ends, 16 pages after the step
+    (16, 16, [40, 200]),                # MHA
+    (4, 32, [100, 7]),                  # group 8
+])
+def test_fused_append_small_batch(gpu, hkv, hq, lens):
+    """Small-batch schedules take the fused path too (one launch per layer)."""
+    from gpu_offloading_amd.kv_cache import PagedKVCache  # noqa: F401
+
+    total = sum((n + 1 + 15) // 16 for n in lens) + 8
+    assert _step_both_ways(gpu, lens, hkv, hq, total, 96)
+
+
 @pytest.mark.parametrize("hkv,hq,lens,total", [
     (8, 32, [3] * 1500, 1600),          # ~6 request ends per segment: append_pieces > 4
-    (2, 8, [100, 7, 250, 64], 100),     # 2 KV heads: one head per workgroup
+    (2, 8, [100, 7, 600, 64], 100),     # 2 KV heads, a 38-page request: one head per workgroup
 ])
 def test_fused_append_falls_back_to_two_calls(gpu, hkv, hq, lens, total):
     assert not _step_both_ways(gpu, lens, hkv, hq, total, 94)
