@@ -455,3 +455,57 @@ def test_xpacked_attention_matches_sdpa_and_partitions_merge(hq, hkv):
     wrong, *_ = orc.paged_attention_xpacked(q, np.ascontiguousarray(kx[:, :, ::-1]), vx, bt,
                                             np.array(lens), scale)
     assert np.abs(wrong - out).max() > 1e-2
+
+
+# --------------------------------------- torch-CPU restatement (baseline)
+def test_torch_cpu_restatement_equals_the_oracle():
+    """oracle/torch_cpu.py (the multi-core CPU baseline bench.py times) gives
+    the oracle's results on the same inputs: bit for bit for append, gather
+    and block swap, within float32 rounding for decode."""
+    from oracle import torch_cpu as tc
+
+    def t16(a):
+        return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)
+
+    rng = np.random.default_rng(40)
+    P, H, Hq, D = 40, 4, 16, 128
+    lens = [1, 16, 17, 100, 0, 255]
+    pool = orc.FifoPagePool(P, len(lens), 16, free_order=rng.permutation(P).tolist())
+    for s, ln in enumerate(lens):
+        pool.ensure_pages(s, (ln + 15) // 16)
+    kc, vc = rand_bf16(rng, (P, 16, H, D)), rand_bf16(rng, (P, 16, H, D))
+    n = sum(lens)
+    k, v = rand_bf16(rng, (n + 3, H, D)), rand_bf16(rng, (n + 3, H, D))
+    step, _ = orc.step_slot_mapping(pool.block_table, range(len(lens)), lens,
+                                    np.zeros(len(lens), np.int64), n)
+    slots = np.concatenate([step, [-1, P * 16, -5]]).astype(np.int64)
+    # append
+    ek, ev = kc.copy(), vc.copy()
+    orc.reshape_and_cache(k, v, ek, ev, slots)
+    gk, gv = t16(kc.copy()), t16(vc.copy())
+    tc.reshape_and_cache(t16(k), t16(v), gk, gv, torch.from_numpy(slots))
+    assert np.array_equal(gk.view(torch.int16).numpy().view(np.uint16), ek)
+    assert np.array_equal(gv.view(torch.int16).numpy().view(np.uint16), ev)
+    # gather
+    ok, ov = orc.gather_kv(ek, ev, pool.block_table, lens)
+    tk, tv = tc.gather_kv(gk, gv, torch.from_numpy(pool.block_table), lens)
+    assert np.array_equal(tk.view(torch.int16).numpy().view(np.uint16), ok)
+    assert np.array_equal(tv.view(torch.int16).numpy().view(np.uint16), ov)
+    # decode
+    q = rand_bf16(rng, (len(lens), Hq, D))
+    indptr, lpl = orc.plan_decode(lens)
+    idx = orc.page_indices(pool.block_table, range(len(lens)), indptr)
+    ro, rl = orc.paged_decode(q, ek, ev, indptr, idx, lpl)
+    to, tl = tc.paged_decode(t16(q), gk, gv, torch.from_numpy(indptr), torch.from_numpy(idx),
+                             torch.from_numpy(lpl))
+    assert np.allclose(to.numpy(), ro, atol=2e-6, rtol=1e-5)
+    assert np.allclose(tl.numpy(), rl, atol=2e-6, rtol=1e-5)
+    # swap: block images and the round trip
+    ids = np.array([idx[3], idx[0], idx[7]], np.int32)
+    img = orc.gather_blocks(ek, ev, ids)
+    timg = tc.gather_blocks(gk, gv, torch.from_numpy(ids))
+    assert np.array_equal(timg.numpy(), img)
+    zk, zv = torch.zeros_like(gk), torch.zeros_like(gv)
+    tc.scatter_blocks(timg, torch.from_numpy(ids), zk, zv)
+    assert torch.equal(zk[ids.astype(np.int64)], gk[ids.astype(np.int64)])
+    assert torch.equal(zv[ids.astype(np.int64)], gv[ids.astype(np.int64)])
