@@ -171,6 +171,8 @@ def load(path: str | None = None) -> ctypes.CDLL:
                 "`python -c 'import __graft_entry__ as g; g.build()'` "
                 "(or gpu_offloading_amd.build.build_library()); "
                 "there is no CPU fallback for the KV-cache ops.")
+        if path is None:
+            _check_fresh()
         lib = ctypes.CDLL(p, mode=ctypes.RTLD_LOCAL)
         for name, (restype, argtypes) in SIGNATURES.items():
             fn = getattr(lib, name)
@@ -179,6 +181,23 @@ def load(path: str | None = None) -> ctypes.CDLL:
         if path is None:
             _lib = lib
         return lib
+
+
+def _check_fresh() -> None:
+    """Refuse a library built from other sources than the ones beside it: its
+    entry points may take other arguments than this table declares."""
+    from .build import STAMP_PATH, source_hash
+
+    try:
+        with open(STAMP_PATH) as f:
+            stamp = f.read().strip()
+    except OSError:
+        raise RuntimeError(f"{LIB_PATH} has no build stamp ({STAMP_PATH}); rebuild it with "
+                           "`python -c 'import __graft_entry__ as g; g.build()'`") from None
+    if stamp != source_hash():
+        raise RuntimeError(f"{LIB_PATH} was built from other sources than "
+                           "gpu_offloading_amd/csrc and include/kvc.h hold now; rebuild it with "
+                           "`python -c 'import __graft_entry__ as g; g.build()'`")
 
 
 def check(func: str, status: int) -> None:

@@ -40,8 +40,27 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build libkvc.so)")
 
 
+STAMP_PATH = LIB_PATH + ".srchash"
+
+
 def sources() -> list[str]:
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+
+
+def source_hash() -> str:
+    """SHA-256 of everything libkvc.so is built from (sources, headers,
+    flags): a library whose stamp differs was built from other sources."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sources() + sorted(glob.glob(os.path.join(CSRC, "*.h"))) + \
+        [os.path.join(INCLUDE, "kvc.h")]
+    for path in files:
+        h.update(os.path.basename(path).encode())
+        with open(path, "rb") as f:
+            h.update(f.read())
+    h.update(" ".join(HIP_FLAGS).encode())
+    return h.hexdigest()
 
 
 def _run(cmd: list[str]) -> tuple[int, list[str]]:
@@ -85,6 +104,8 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> str:
     if verbose and msgs:
         print("\n".join(msgs), file=sys.stderr)
     os.replace(tmp, LIB_PATH)
+    with open(STAMP_PATH, "w") as f:
+        f.write(source_hash() + "\n")
     return LIB_PATH
 
 

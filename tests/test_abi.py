@@ -386,3 +386,21 @@ def test_prefill_plan_reports_capacity_and_rejects_bad_input(lib):
     assert st == 0 and sched.num_items == 0
     assert lib.kvc_batch_prefill_run(ctypes.byref(sched), None, None, 4096, None, None, 16384,
                                      1024, 1, None, 0, 0.1, None, 4096, None, None) == 0
+
+
+def test_a_library_built_from_other_sources_is_refused(tmp_path, monkeypatch):
+    """The build stamps libkvc.so with a hash of its sources; loading checks it,
+    so a library whose entry points may differ from this ctypes table is never
+    called."""
+    from gpu_offloading_amd import build
+
+    assert open(build.STAMP_PATH).read().strip() == build.source_hash()
+    _lib._check_fresh()                                     # the current build passes
+    stale = tmp_path / "stamp"
+    stale.write_text("0" * 64 + "\n")
+    monkeypatch.setattr(build, "STAMP_PATH", str(stale))
+    with pytest.raises(RuntimeError, match="other sources"):
+        _lib._check_fresh()
+    monkeypatch.setattr(build, "STAMP_PATH", str(tmp_path / "missing"))
+    with pytest.raises(RuntimeError, match="no build stamp"):
+        _lib._check_fresh()

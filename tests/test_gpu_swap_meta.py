@@ -211,3 +211,53 @@ def test_cfg5_swap_under_decode_round_trip(gpu):
         for a, b in zip(before[layer], after[layer]):
             assert torch.equal(a, b)
     assert h.bytes_per_direction == L * len(victims) * 128 * 2 * 16 * 16 * 128 * 2
+
+
+@pytest.mark.parametrize("staging_mib", [8, 64])
+def test_c_abi_swap_round_trip_and_rate(gpu, staging_mib):
+    """kvc_swap_out / kvc_swap_in through the C entry points: one layer of
+    configuration 5's eviction (4096 of 8192 OLMoE blocks, 128 KiB of K+V
+    each: 512 MiB each way) through an 8 or 64 MiB staging buffer, restored
+    into other block ids bit for bit (the oracle's block image).  With 64 MiB
+    of staging a C caller gets the host link's rate (>= 53 GB/s each way)."""
+    from gpu_offloading_amd import _lib
+
+    print(f"c-abi swap: 512 MiB each way, {staging_mib} MiB staging", flush=True)
+    lib = _lib.load()
+    nb, n = 8192, 4096
+    g = torch.Generator(device=gpu).manual_seed(60)
+    kc = torch.empty(nb, 16, 16, 128, dtype=torch.bfloat16, device=gpu).normal_(generator=g)
+    vc = torch.empty_like(kc).normal_(generator=g)
+    bb = ops.block_bytes(kc)
+    src = torch.tensor(workloads.randperm(nb, 61)[:n], dtype=torch.int32, device=gpu)
+    dst = torch.tensor(workloads.randperm(nb, 62)[:n], dtype=torch.int32, device=gpu)
+    staging = torch.empty(staging_mib << 20, dtype=torch.uint8, device=gpu)
+    host = torch.empty(n * 2 * bb, dtype=torch.uint8, pin_memory=True)
+    ref = orc.gather_blocks(u16(kc), u16(vc), src.cpu().numpy())
+    side = torch.cuda.Stream(device=gpu)
+    k2, v2 = torch.zeros_like(kc), torch.zeros_like(vc)
+    rates = {}
+    for direction in ("out", "in"):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(side)
+        if direction == "out":
+            st = lib.kvc_swap_out(kc.data_ptr(), vc.data_ptr(), kc.stride(0) * 2, bb, nb,
+                                  src.data_ptr(), n, staging.data_ptr(), staging.numel(),
+                                  host.data_ptr(), None, side.cuda_stream)
+        else:
+            st = lib.kvc_swap_in(host.data_ptr(), dst.data_ptr(), n, k2.data_ptr(),
+                                 v2.data_ptr(), kc.stride(0) * 2, bb, nb, staging.data_ptr(),
+                                 staging.numel(), None, side.cuda_stream)
+        assert st == 0, lib.kvc_last_error()
+        e1.record(side)
+        e1.synchronize()
+        rates[direction] = n * 2 * bb / (e0.elapsed_time(e1) * 1e-3) / 1e9
+        if direction == "out":
+            assert np.array_equal(host.numpy().reshape(ref.shape), ref)
+    got = orc.gather_blocks(u16(k2), u16(v2), dst.cpu().numpy())
+    assert np.array_equal(got, ref)
+    print(f"c-abi swap GB/s ({staging_mib} MiB staging): out {rates['out']:.1f}, "
+          f"in {rates['in']:.1f}", flush=True)
+    if staging_mib >= 64:
+        assert rates["out"] >= 53 and rates["in"] >= 53, rates
