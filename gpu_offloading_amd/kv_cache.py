@@ -545,6 +545,163 @@ class PagedKVCache:
         self._step_slots = slots[:b]
         return slots
 
+    def prepare_step(self, decode_seq_ids: Sequence[int] = (),
+                     prefill_seq_ids: Sequence[int] = (), prefill_lens: Sequence[int] = (),
+                     continuation_seq_ids: Sequence[int] = (),
+                     continuation_lens: Sequence[int] = (),
+                     graph_n: Optional[int] = None) -> torch.Tensor:
+        """Setup of a mixed step, the engine's ``step()`` (moe_engine.py:2555-2742,
+        piecewise setup :3475-3556, continuation plan :3649-3728), with one
+        host-to-device copy of all its metadata.
+
+        Tokens are laid out ``[decode | new prefill | continuation]``: one per
+        decode request (at its current length), ``prefill_lens[i]`` from
+        position 0 for each new prompt (its length must be 0), and
+        ``continuation_lens[i]`` from each continuation's current length.  The
+        returned slot mapping (int64, padded with -1 to ``graph_n`` tokens)
+        serves ``append`` of the step's K/V.  Afterwards the lengths are
+        decode + 1, prompt length and offset + chunk; the decode wrapper is
+        planned over the decode requests (``decode``: q rows in
+        ``decode_seq_ids`` order) and the prefill wrapper over the
+        continuations (``prefill``: their q rows, chunk after chunk).  New
+        prompts attend over their own contiguous K/V outside the paged cache,
+        as in the engine.  Pages must already cover every new token."""
+        self._require_gpu()
+        dec = [int(s) for s in decode_seq_ids]
+        pre = [int(s) for s in prefill_seq_ids]
+        con = [int(s) for s in continuation_seq_ids]
+        plen = [int(n) for n in prefill_lens]
+        clen = [int(n) for n in continuation_lens]
+        if len(plen) != len(pre) or len(clen) != len(con):
+            raise ValueError("one length per prefill / continuation sequence")
+        if any(n <= 0 for n in plen + clen):
+            raise ValueError("prefill and continuation lengths must be positive")
+        D, P, C = len(dec), len(pre), len(con)
+        ids = self._check_seq_ids(dec + pre + con)
+        R = len(ids)
+        counts = np.array([1] * D + plen + clen, dtype=np.int64)
+        n_tok = int(counts.sum())
+        graph_n = n_tok if graph_n is None else int(graph_n)
+        if graph_n < n_tok:
+            raise ValueError(f"graph_n ({graph_n}) is smaller than the step's {n_tok} tokens")
+        self._step_slots = None
+        if R == 0:
+            return torch.full((graph_n,), -1, dtype=torch.int64, device=self.device)
+        self._sync_seqs(ids.tolist())
+        lens_all = self._seq_lens_cpu.numpy()
+        ms, ps = self.max_seqs, self.page_size
+        before = lens_all[ids].astype(np.int64)
+        if P and (before[D:D + P] != 0).any():
+            raise RuntimeError("a new prefill's sequence must be empty (free_seq it first)")
+        after = before + counts
+        if int(after.max()) > self.max_pages_per_seq * ps:
+            raise RuntimeError(f"a sequence would exceed max_seq_len ({self.max_pages_per_seq * ps})")
+        if self._dynamic_pages:
+            short = [int(s) for s, n in zip(ids, after) if self._pool.seq_pages(int(s)) * ps < n]
+            if short:
+                raise RuntimeError(f"sequences {short} have no page for their new tokens "
+                                   "(ensure_pages first)")
+        d_after, c_after = after[:D], after[D + P:]
+
+        def indptr_lpl(lens):
+            ip = np.zeros(len(lens) + 1, np.int32)
+            np.cumsum((lens + ps - 1) // ps, out=ip[1:])
+            lpl = lens % ps
+            return ip, np.where((lpl == 0) & (lens != 0), ps, lpl).astype(np.int32)
+
+        # One pinned int32 image:
+        #   ids[R] | qsl[R+1] | lens_before[ms] | lens_after[ms]
+        #   | decode kv_indptr[D+1] | decode last_page_len[D]
+        #   | continuation qo_indptr[C+1] | kv_indptr[C+1] | last_page_len[C]
+        #   | block-table positions (int64) | page ids
+        #   | decode schedule | prefill schedule (16-byte aligned each)
+        pend = self._peek_bt_pending()
+        u = 0 if pend is None else len(pend[0])
+        dw, pw = self._decode_wrapper, self._prefill_wrapper
+        o_qsl = R
+        o_lb = o_qsl + R + 1
+        o_la = o_lb + ms
+        o_dip = o_la + ms
+        o_dlpl = o_dip + D + 1
+        o_cqo = o_dlpl + D
+        o_cip = o_cqo + C + 1
+        o_clpl = o_cip + C + 1
+        o_pos = (o_clpl + C + 1) // 2 * 2
+        o_val = o_pos + 2 * u
+        o_dplan = (o_val + u + 3) // 4 * 4
+        group = self.num_heads // self.num_kv_heads
+        pcap = pw._plan_capacity(np.asarray(clen), group) if C else 0
+        dcap = dw._plan_capacity(D) if D else 0
+        while True:
+            o_pplan = o_dplan + dcap
+            hs = torch.empty(o_pplan + pcap, dtype=torch.int32, pin_memory=True)
+            h = hs.numpy()
+            h[:R] = ids
+            h[o_qsl] = 0
+            np.cumsum(counts, out=h[o_qsl + 1:o_lb])
+            h[o_lb:o_la] = lens_all
+            h[o_la:o_dip] = lens_all
+            h[o_la + ids] = after
+            dip, dlpl = indptr_lpl(d_after)
+            h[o_dip:o_dlpl] = dip
+            h[o_dlpl:o_cqo] = dlpl
+            h[o_cqo] = 0
+            np.cumsum(np.asarray(clen, np.int64), out=h[o_cqo + 1:o_cip])
+            cip, clpl = indptr_lpl(c_after)
+            h[o_cip:o_clpl] = cip
+            h[o_clpl:o_clpl + C] = clpl
+            if u:
+                h[o_pos:o_pos + 2 * u].view(np.int64)[:] = pend[0]
+                h[o_val:o_val + u] = pend[1]
+            dsched = None
+            if D:
+                dsched = dw._schedule_into(h[o_dip:o_dlpl], h[o_dlpl:o_cqo], D, self.num_heads,
+                                           self.num_kv_heads, self.head_dim, ps,
+                                           hs[o_dplan:o_pplan])
+                if dsched.plan_ints > dcap:
+                    dcap = (dsched.plan_ints + 3) // 4 * 4
+                    continue
+            break
+        psched = None
+        if C:
+            psched = pw._schedule_into(h[o_cqo:o_cip], h[o_cip:o_clpl], h[o_clpl:o_clpl + C], C,
+                                       self.num_heads, self.num_kv_heads, self.head_dim, ps,
+                                       True, hs[o_pplan:])
+        self._check_page_counts(np.concatenate([(d_after + ps - 1) // ps,
+                                                (c_after + ps - 1) // ps]))
+
+        dm = hs.to(self.device, non_blocking=True)           # the step's one H2D copy
+        if u:
+            self._bt.view(-1).scatter_(0, dm[o_pos:o_val].view(torch.int64), dm[o_val:o_val + u])
+            self._bt_pending.clear()
+        ids_d = dm[:R]
+        slots = torch.empty(graph_n, dtype=torch.int64, device=self.device)
+        ops.compute_slot_mapping(self._bt, ids_d, dm[o_qsl:o_lb], dm[o_lb:o_la], n_tok, slots,
+                                 block_size=ps)
+        self.seq_lens.copy_(dm[o_la:o_dip])
+        # A wrapper with no requests this step keeps no plan: a run() would
+        # otherwise attend with the previous step's.
+        if not D:
+            dw._sched = None
+        if not C:
+            pw._sched = None
+        if D:
+            total = int(dip[-1])
+            ops.copy_page_indices(self._bt, dm[o_dip:o_dlpl], self._plan_indices_gpu,
+                                  seq_ids=ids_d[:D])
+            dw._install(dsched, dm[o_dplan:o_dplan + dcap], dm[o_dip:o_dlpl],
+                        dm[o_dlpl:o_cqo], self._plan_indices_gpu[:total], self.num_heads,
+                        self.num_kv_heads, self.head_dim, ps)
+        if C:
+            total = int(cip[-1])
+            ops.copy_page_indices(self._bt, dm[o_cip:o_clpl], self._prefill_indices_gpu,
+                                  seq_ids=ids_d[D + P:])
+            pw._install(psched, dm[o_pplan:o_pplan + max(pcap, 8)],
+                        self._prefill_indices_gpu[:max(total, 1)], int(sum(clen)),
+                        self.num_heads, self.num_kv_heads, self.head_dim, ps)
+        lens_all[ids] = after
+        return slots
+
     # ------------------------------------------------------- per-layer ops
     def append(self, layer: int, key: torch.Tensor, value: torch.Tensor,
                slot_mapping: torch.Tensor) -> None:

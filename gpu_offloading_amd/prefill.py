@@ -128,6 +128,37 @@ class BatchPrefillWithPagedKVCacheWrapper:
 
     begin_forward = plan
 
+    # ------------------------------------------------- in-package fast path
+    @staticmethod
+    def _plan_capacity(q_lens: np.ndarray, group: int) -> int:
+        """int32 entries to reserve for the plan image (16-byte multiple)."""
+        tile = 128 // group if group in (1, 2, 4, 8) else 1
+        ql = np.maximum(np.asarray(q_lens, np.int64), 0)
+        cap = int(np.sum((ql + tile - 1) // tile)) * 8 + 8
+        return (cap + 3) // 4 * 4
+
+    def _schedule_into(self, qo: np.ndarray, kv: np.ndarray, lpl: np.ndarray, batch: int,
+                       num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
+                       causal: bool, image: torch.Tensor) -> _lib.KvcPrefillSchedule:
+        """kvc_prefill_plan into the pinned int32 ``image`` (sized by
+        ``_plan_capacity``)."""
+        sched = _lib.KvcPrefillSchedule()
+        _lib.call("kvc_prefill_plan", qo.ctypes.data, kv.ctypes.data, lpl.ctypes.data, batch,
+                  num_qo_heads, num_kv_heads, head_dim, page_size, 1 if causal else 0,
+                  sched, image.data_ptr(), image.numel())
+        return sched
+
+    def _install(self, sched: _lib.KvcPrefillSchedule, plan_dev: torch.Tensor,
+                 indices_dev: torch.Tensor, total_q: int, num_qo_heads: int, num_kv_heads: int,
+                 head_dim: int, page_size: int) -> None:
+        """Adopt a schedule whose image and page indices are already on the
+        device (staged by the caller in stream order before the next run)."""
+        self._sched = sched
+        self._plan_dev = plan_dev
+        self._indices = indices_dev
+        self._plan_args = (total_q, num_qo_heads, num_kv_heads, head_dim, page_size)
+        self._sm_scale = 1.0 / math.sqrt(head_dim)
+
     @property
     def schedule(self) -> _lib.KvcPrefillSchedule:
         return self._sched
