@@ -76,10 +76,8 @@ struct DecodeArgs {
   int64_t block_stride;    // elements between cache blocks
   int64_t token_stride;    // elements between tokens of a block
   int64_t num_blocks;
-  const int32_t* indptr;
   const int32_t* indices;
   int64_t num_indices;
-  const int32_t* last_page_len;
   const int4* segments;    // [S]: (first piece, end piece, first slot, pages)
   int32_t total_pages;     // pages of the whole batch
   int32_t num_segments;
@@ -1375,9 +1373,10 @@ int decode_run(const kvc_decode_schedule* sched, const int32_t* plan, const void
   KVC_REQUIRE(sched, KVC_ERR_INVALID_ARG, "null schedule");
   const int batch = sched->batch;
   if (batch == 0) return ok();
-  // indices may be null (an empty tensor) when no request has a page.
-  KVC_REQUIRE(plan && q && key_cache && value_cache && indptr &&
-                  (indices || sched->total_pages == 0) && last_page_len && out,
+  // indices may be null (an empty tensor) when no request has a page; the
+  // device indptr / last_page_len are not read (the plan image carries both).
+  KVC_REQUIRE(plan && q && key_cache && value_cache && (indices || sched->total_pages == 0) &&
+                  out,
               KVC_ERR_INVALID_ARG, "null pointer");
   const int Hq = sched->num_qo_heads, Hkv = sched->num_kv_heads, D = sched->head_dim;
   KVC_REQUIRE(Hkv > 0 && Hq % Hkv == 0, KVC_ERR_INVALID_ARG, "bad head counts");
@@ -1425,10 +1424,8 @@ int decode_run(const kvc_decode_schedule* sched, const int32_t* plan, const void
   a.block_stride = cache_block_stride;
   a.token_stride = cache_token_stride;
   a.num_blocks = num_blocks;
-  a.indptr = indptr;
   a.indices = indices;
   a.num_indices = num_indices;
-  a.last_page_len = last_page_len;
   a.segments = reinterpret_cast<const int4*>(plan);
   a.pieces = reinterpret_cast<const int4*>(plan + sched->pieces_offset);
   a.total_pages = sched->total_pages;

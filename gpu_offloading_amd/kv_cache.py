@@ -27,6 +27,7 @@ from . import ops
 from .allocator import PagePool, pages_needed
 from .decode import BatchDecodeWithPagedKVCacheWrapper
 from .prefill import BatchPrefillWithPagedKVCacheWrapper
+from .swap_ledger import SwapLedger
 
 __all__ = ["PagedKVCache", "SwapHandle"]
 
@@ -140,8 +141,7 @@ class PagedKVCache:
         self._staging_free: list[Optional[torch.cuda.Event]] = [None, None]
         self._swap_stream: Optional[torch.cuda.Stream] = None
         self._copy_stream: Optional[torch.cuda.Stream] = None
-        self._pending_free: list[tuple[torch.cuda.Event, list[int], list]] = []
-        self._pending_in: dict[int, torch.cuda.Event] = {}
+        self._swaps = SwapLedger()   # swap-outs / restores still in flight
 
     def _init_step_buffers(self) -> None:
         """Decode workspace + wrapper and the device page-index buffer
@@ -279,9 +279,8 @@ class PagedKVCache:
         whoever is given the pages next (an append on the current stream, a
         swap on the side stream, which waits for the current one) writes
         after the restore."""
-        ev = self._pending_in.pop(seq_id, None)
-        if ev is not None:
-            torch.cuda.current_stream(self.device).wait_event(ev)
+        if self._swaps.pending_in:
+            self._swaps.on_free(seq_id, torch.cuda.current_stream(self.device))
         self._seq_lens_cpu[seq_id] = 0
         self.seq_lens[seq_id] = 0
         if self._dynamic_pages:
@@ -300,8 +299,7 @@ class PagedKVCache:
             self._pool.reset()
             self._bt_pending.clear()
             self._bt.fill_(-1)
-        self._pending_free.clear()
-        self._pending_in.clear()
+        self._swaps.clear()
 
     # ----------------------------------------------------- snapshot / fill
     def fill_kv_random(self, std: float = 0.01, generator: Optional[torch.Generator] = None) -> None:
@@ -339,13 +337,8 @@ class PagedKVCache:
 
     def _sync_seqs(self, seq_ids: Sequence[int]) -> None:
         """Order the current stream after pending swap-ins of these sequences."""
-        if not self._pending_in:
-            return
-        cur = torch.cuda.current_stream(self.device)
-        for sid in seq_ids:
-            ev = self._pending_in.pop(int(sid), None)
-            if ev is not None:
-                cur.wait_event(ev)
+        if self._swaps.pending_in:
+            self._swaps.before_use(seq_ids, torch.cuda.current_stream(self.device))
 
     def slot_mapping(self, seq_ids: Sequence[int], num_new_tokens: Sequence[int],
                      graph_n: Optional[int] = None) -> torch.Tensor:
@@ -864,17 +857,7 @@ class PagedKVCache:
     def _reclaim(self, need: int = 0) -> None:
         """Return pages of finished swap-outs to the free list; block on the
         oldest pending swap-out only if the pool cannot serve ``need`` pages."""
-        still = []
-        for ev, pages, keep in self._pending_free:
-            if ev.query():
-                self._pool.give_back(pages)
-            else:
-                still.append((ev, pages, keep))
-        self._pending_free = still
-        while self._pending_free and self._pool.pages_free < need:
-            ev, pages, keep = self._pending_free.pop(0)
-            ev.synchronize()
-            self._pool.give_back(pages)
+        self._swaps.reclaim(self._pool, need)
 
     def synchronize_swaps(self) -> None:
         for st in (self._swap_stream, self._copy_stream):
@@ -919,7 +902,7 @@ class PagedKVCache:
         self._side_stream().wait_stream(cur)
         start, ev = self._pipelined_swap(True, ids_t, n, host)
         # The host buffer must outlive the D2H copy even if the handle is dropped.
-        self._pending_free.append((ev, ids, [ids_t, host]))
+        self._swaps.add_swap_out(ev, ids, [ids_t, host])
         return SwapHandle(seq_ids, lens, npages, ids_t, host, ev, out_start=start, num_bytes=nbytes)
 
     def swap_in(self, handle: SwapHandle, wait: bool = False,
@@ -956,12 +939,10 @@ class PagedKVCache:
         self._dma_stream().wait_stream(side)
         start, ev = self._pipelined_swap(False, dst_t, len(dst), handle.host)
         handle.in_start = start
-        self._pending_free.append((ev, [], [dst_t, handle.host]))
+        self._swaps.add_swap_in(ev, targets, [dst_t, handle.host])
         handle.in_event = ev
         handle.dst_block_ids = dst_t
         handle.restored = True
         handle.seq_ids = targets
-        for sid in targets:
-            self._pending_in[sid] = ev
         if wait:
             self._sync_seqs(targets)

@@ -158,7 +158,14 @@ int kvc_decode_plan(const int32_t* indptr_host, const int32_t* last_page_len_hos
 int64_t kvc_decode_workspace_bytes(int32_t batch, int32_t num_qo_heads,
                                    int32_t head_dim, int32_t max_partitions);
 
-/* plan: the device copy (16-byte aligned) of the image kvc_decode_plan wrote. */
+/* plan: the device copy (16-byte aligned) of the image kvc_decode_plan wrote.
+ * The kernels take every request's page span and last-page length from the
+ * plan image (kvc_decode_plan copies them from the host indptr and
+ * last_page_len); the device indptr and last_page_len arguments are accepted
+ * for symmetry with FlashInfer's run() and are not read (they may be null).
+ * So lengths changed on the device after kvc_decode_plan are not seen: plan
+ * again, as FlashInfer requires after every change of the lengths.  The page
+ * ids themselves (indices) are read on the device at run time. */
 int kvc_batch_decode_run(
     const kvc_decode_schedule* schedule, const int32_t* plan,
     const void* q, int64_t q_batch_stride,
