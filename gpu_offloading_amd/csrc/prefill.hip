@@ -18,22 +18,25 @@
 //                 a lane ends up owning ONE query row (column l%32) and 32 of
 //                 the tile's 64 keys, the other 32 being in lane l^32;
 //   online softmax per lane (row), one exchange with lane l^32 for the row
-//                 max and sum; the lane's P values are already laid out as
-//                 the B operand of the next product (see the key order below);
+//                 max (the row sum stays split between the two lanes until
+//                 the end); the lane's P values are already laid out as the
+//                 B operand of the next product (see the key order below);
 //   O^T += V^T P^T  (head dims x query rows): 4 dim blocks x 4 k-steps of 16
 //                 keys; O^T's columns are query rows too, so the per-row
 //                 rescale by exp2(m_old - m_new) is a per-lane multiply.
 // Key order inside a 16-key k-step: lane half h supplies k = 8h..8h+7, which
-// the S^T accumulator layout gives as keys {4h..4h+3, 8+4h..8+4h+3}.  V^T is
-// therefore stored in LDS with its 4-key groups 1 and 2 of every 16 swapped,
-// so each lane's 8 keys are one 16-byte read.
+// the S^T accumulator layout gives as keys {4h..4h+3, 8+4h..8+4h+3}; the V^T
+// operand is read in that order.
 //
-// Staging: K as [key][dim] rows padded to 272 B (the q.k reads of 32 rows hit
-// distinct banks), V transposed to [dim][key] rows padded to 144 B; each thread
-// packs 4 keys x 8 dims with v_perm and writes 8-byte runs.  Two LDS tile
-// buffers: tile t+1 is loaded into registers while tile t is computed, one
-// barrier per tile.  Rows past the end of the cache are staged as zeros, so a
-// masked key contributes exactly 0 (even if the page holds NaN bits).
+// Staging: K and V go from memory straight into LDS (global_load_lds_dwordx4,
+// buffer_load_dwordx4 ... lds) as unpadded [key][dim] rows whose 16-byte
+// chunks are XOR-swizzled by key, so that the MFMA operand reads hit distinct
+// banks: K as 16-byte reads of one key's dims, V^T through the transposing
+// ds_read_b64_tr_b16.  Two LDS buffers per operand, K staged two tiles ahead
+// and V one, one barrier per tile.  V rows past the end of the cache or in a
+// missing page load as zeros (the buffer load is bounded to the page's valid
+// tokens), so a masked key contributes exactly 0 even if the page holds NaN
+// bits.
 #include "kvc_common.h"
 
 #include <algorithm>
@@ -46,6 +49,10 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
 constexpr int kThreads = 256;
 constexpr int kWaveRows = 32;                 // query rows per wave
@@ -53,10 +60,15 @@ constexpr int kTileRows = 4 * kWaveRows;      // query rows per workgroup
 constexpr int kKeys = 64;                     // keys per tile
 constexpr int kPage = 16;
 constexpr int kD = 128;
-constexpr int kKPitch = kD * 2 + 16;          // bytes per K row in LDS
-constexpr int kVPitch = kKeys * 2 + 16;       // bytes per V^T row in LDS
+constexpr int kKRow = kD * 2;                // bytes per K or V row in LDS (unpadded)
 constexpr int kItemInts = 8;
 constexpr float kRescaleLog2 = 8.f;           // lazy-rescale threshold (base 2)
+// Word 3 of a raw buffer resource (32-bit data, no swizzle): loads past
+// num_records return zeros.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+// s_waitcnt vmcnt(0) with the other counters unconstrained (gfx9 encoding:
+// vmcnt [3:0],[15:14]; expcnt [6:4]; lgkmcnt [11:8]).
+constexpr int kWaitVmcnt0 = 0x0F70;
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kLog2e = 1.44269504088896340736f;
 
@@ -80,18 +92,13 @@ struct PrefillArgs {
   float* lse;              // [total_q][Hq] natural log, may be null
 };
 
-struct alignas(16) TileBuf {
-  uint8_t k[kKeys * kKPitch];
-  uint8_t vt[kD * kVPitch];
-};
-
-// Position of key `k` (0..63) of a tile inside its V^T row: 4-key groups 1
-// and 2 of every 16 are swapped.
-__device__ __forceinline__ int vt_pos(int k) {
-  const int grp = (k >> 2) & 3;
-  const int sw = grp == 1 ? 2 : grp == 2 ? 1 : grp;
-  return (k & ~15) | (sw << 2) | (k & 3);
-}
+// K rows of 256 B whose 16-byte chunks are XOR-swizzled by key: chunk c of
+// key k sits in slot c ^ (k % 16).
+struct alignas(16) KTile { uint8_t b[kKeys * kKRow]; };
+// V rows of 256 B, natural [key][dim] layout, 16-byte chunks XOR-swizzled
+// as chunk c of key k in slot c ^ 4(k % 4): the transposing reads of four
+// consecutive keys then hit distinct banks.
+struct alignas(16) VTile { uint8_t b[kKeys * kKRow]; };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, v);
@@ -103,17 +110,21 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Two waves per SIMD (<= 256 VGPRs, no AGPRs): with one, the LDS-read and
-// softmax latencies of a wave are exposed (262 -> 443 TFLOP/s measured on an
-// 8 x 2048-token causal batch).  The softmax is the other limit -- the VALU
-// runs beside the MFMAs of the other wave -- so it is kept lean: per-key
-// tests only on boundary tiles, the scale folded into one FMA per score, the
-// O rescale skipped unless a row max grows by more than 2^8, and P packed to
-// bf16 with v_cvt_pk_bf16_f32 (443 -> 575 TFLOP/s on the same batch).
+// Two waves per SIMD (<= 256 VGPRs, no AGPRs).  The softmax's VALU work per
+// key tile is about as long as the tile's 32 MFMAs, so each wave runs them
+// side by side: step j computes the softmax of tile j while the MFMAs of the
+// scores of tile j+1 run, then P_j V_j while the next tiles are staged.  The
+// softmax is kept lean: per-key tests only on boundary tiles, the scale folded
+// into one FMA per score, the O rescale skipped unless a row max grows by
+// more than 2^8, P packed to bf16 with v_cvt_pk_bf16_f32 and summed from the
+// packed pairs with v_dot2_f32_bf16, the row max exchanged between the two
+// lane halves with v_permlane32_swap, and the row sum kept per lane half
+// until the end.
 template <int G>
 __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int kTokPerWave = kWaveRows / G;
-  __shared__ TileBuf tiles[2];
+  __shared__ KTile ktiles[2];
+  __shared__ VTile vtiles[2];
 
   const int h = blockIdx.y;
   const int4 it0 = a.items[2 * blockIdx.x];
@@ -121,7 +132,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   const int tok0 = it0.y, q_len = it0.z, kv_len = it0.w;
   const int q_off = it1.x, page_off = it1.y, ntiles = it1.z, npages = it1.w;
 
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
   const int lane = threadIdx.x & 63;
   const int r = lane & 31;
   const int half = lane >> 5;
@@ -146,102 +157,132 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
     }
   }
 
-  // Staging roles.  K: thread t copies 16-byte chunk t%16 of token t/16 of
-  // each of the tile's 4 pages.  V: thread t copies chunk t/16 of tokens
-  // 4(t%16 % 4) .. +3 of page (t%16)/4 -- four consecutive keys, so that it
-  // can write them transposed as 8-byte runs.
-  const int t = threadIdx.x;
-  const int k_tok = t >> 4, k_chunk = t & 15;
-  const int v_grp = t & 15, v_chunk = t >> 4;
-  const int v_page = v_grp >> 2, v_tok = (v_grp & 3) * 4;
   const int64_t head_off = int64_t(h) * kD;
   const char* kbase = reinterpret_cast<const char*>(a.k_cache);
   const char* vbase = reinterpret_cast<const char*>(a.v_cache);
-  const int64_t blk_bytes = a.block_stride * 2;
   const int64_t tok_bytes = a.token_stride * 2;
-  const uint32_t k_lane_off = uint32_t(k_tok * tok_bytes + (head_off + k_chunk * 8) * 2);
+  // K (direct to LDS): lane L fetches key 4*wave + L/16 of each page, the
+  // chunk whose swizzled slot is L%16.
+  const int k_key = 4 * wave + (lane >> 4);
+  const uint32_t k_lane_off =
+      uint32_t(k_key * tok_bytes + (head_off + ((lane & 15) ^ (k_key & 15)) * 8) * 2);
+  // V the same way, with its own swizzle.
+  const uint32_t v_lane_off =
+      uint32_t(k_key * tok_bytes + (head_off + ((lane & 15) ^ (4 * (k_key & 3))) * 8) * 2);
+  // Every global_load_lds of this wave has written LDS (vmcnt 0).
+  auto wait_dma = []() __attribute__((always_inline)) { __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); };
 
-  uint4 kreg[4], vreg[4];
-  // Page ids of a tile, fetched one iteration before its K/V loads need them
-  // (four independent loads at clamped addresses; validity applied after),
-  // so no load waits on an id.
-  // Nothing reads the loaded ids until load_tile, so no wait sits here;
-  // which of them exist is decided from the page index alone.
-  struct TileIds { int32_t v[4]; int exists; };
+  // Page ids of a tile as loaded: four independent loads at clamped
+  // addresses, fetched well before their K/V loads need them.  All index
+  // arithmetic is 32-bit so that it stays on the scalar unit (the host keeps
+  // every page index below 2^31).
+  const int32_t last_index = int32_t(min(a.num_indices - 1, int64_t(INT32_MAX)));
+  const int32_t num_blocks32 = int32_t(min(a.num_blocks, int64_t(INT32_MAX)));
+  struct RawIds { int32_t v[4]; };
   auto fetch_ids = [&](int tile) __attribute__((always_inline)) {
-    TileIds t;
-    t.exists = 0;
-    const int64_t last = a.num_indices - 1;
+    RawIds t;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int p = tile * 4 + u;
-      t.v[u] = a.indices[min(int64_t(page_off) + p, last)];
-      t.exists |= (p < npages && int64_t(page_off) + p <= last) ? (1 << u) : 0;
-    }
+    for (int u = 0; u < 4; ++u) t.v[u] = a.indices[min(page_off + tile * 4 + u, last_index)];
     return t;
   };
-  // load_tile returns a mask whose bit u says page u of the tile is real.
-  auto load_tile = [&](const TileIds& t) __attribute__((always_inline)) {
+  // Wave-uniform page ids of a tile; bit u of `ok` says page u is real
+  // (inside the request and the cache), the others read block 0 and are
+  // masked.  (Plain scalars, not an array: a copy carried across steps must
+  // stay in registers.)
+  struct Pages { int32_t id0, id1, id2, id3; int ok; };
+  auto resolve = [&](const RawIds& t, int tile) __attribute__((always_inline)) {
+    int32_t id[4];
     int ok = 0;
-    int32_t ids[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int32_t id = __builtin_amdgcn_readfirstlane(t.v[u]);
-      const bool good = ((t.exists >> u) & 1) && id >= 0 && id < a.num_blocks;
+      const int32_t v = __builtin_amdgcn_readfirstlane(t.v[u]);
+      const int p = tile * 4 + u;
+      const bool good = p < npages && page_off + p <= last_index && v >= 0 && v < num_blocks32;
       ok |= good ? (1 << u) : 0;
-      ids[u] = good ? id : 0;
+      id[u] = good ? v : 0;
     }
+    return Pages{id[0], id[1], id[2], id[3], ok};
+  };
+  // Start of a cache block (the host keeps a block under 4 GiB).
+  const uint32_t blk32 = uint32_t(a.block_stride * 2);
+  auto block_at = [&](const char* base, int32_t id) __attribute__((always_inline)) {
+    return base + uint64_t(uint32_t(id)) * blk32;
+  };
+  // Direct loads from memory into LDS (global_load_lds_dwordx4 and
+  // buffer_load_dwordx4 ... lds, one 16-byte chunk per lane, lane L at LDS
+  // offset 16L from the wave-uniform address in M0).  They are issued as
+  // inline assembly so that the compiler does not make every later LDS read
+  // wait for them (it cannot tell the buffer being filled from the one being
+  // read); the step waits for them itself (vmcnt 0) before the barrier that
+  // publishes the tiles.  No compiler-generated code here uses M0.
+  auto lds_addr = [](const void* p) __attribute__((always_inline)) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t*)p));
+  };
+
+  // K goes straight from memory into LDS (global_load_lds_dwordx4): one
+  // instruction of a wave fills 1 KB of LDS, lane L's 16 bytes at offset
+  // 16L, so wave w fills keys 16u + 4w .. +3 of page u, and lane L fetches
+  // the chunk that belongs in slot L%16 of key 4w + L/16 of the page.  The
+  // loads are waited for (vmcnt) before the barrier that publishes the tile.
+  auto dma_k = [&](KTile& buf, const Pages& p) __attribute__((always_inline)) {
+    const int32_t id[4] = {p.id0, p.id1, p.id2, p.id3};
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const char* blk = kbase + int64_t(ids[u]) * blk_bytes;  // uniform
-      kreg[u] = *reinterpret_cast<const uint4*>(blk + k_lane_off);
+      const char* blk = block_at(kbase, id[u]);
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                   :: "s"(lds_addr(buf.b + (u * kPage + 4 * wave) * kKRow)), "v"(k_lane_off),
+                      "s"(blk) : "memory");
     }
-    int32_t vid = ids[0];
-#pragma unroll
-    for (int u = 1; u < 4; ++u) vid = v_page == u ? ids[u] : vid;
-    const char* vp = vbase + int64_t(vid) * blk_bytes + (head_off + v_chunk * 8) * 2;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      vreg[e] = *reinterpret_cast<const uint4*>(vp + (v_tok + e) * tok_bytes);
-    return ok;
   };
-  // Keys past the cache or in a missing page are staged as zeros: a mask
-  // (v_and) on tiles that have such keys, nothing on the others.
-  auto stage_tile = [&](TileBuf& buf, int tile, int ok) __attribute__((always_inline)) {
-    const int key0 = tile * kKeys;
-    if (ok != 0xF || key0 + kKeys > kv_len) {
+  // V goes into LDS the same way, through a buffer load bounded to the
+  // page's valid tokens: lanes past kv_len or in a missing page get zeros
+  // (a P of 0 times V bits that happen to be NaN would not be 0).  K needs
+  // no such care: a key's score depends on its own K row only, and tiles
+  // holding such keys are processed with the per-key tests, which never
+  // read its score.
+  auto dma_v = [&](VTile& buf, const Pages& p, int tile) __attribute__((always_inline)) {
+    const int32_t id[4] = {p.id0, p.id1, p.id2, p.id3};
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t m = (((ok >> u) & 1) && key0 + u * kPage + k_tok < kv_len) ? ~0u : 0u;
-        kreg[u].x &= m; kreg[u].y &= m; kreg[u].z &= m; kreg[u].w &= m;
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = v_page * kPage + v_tok + e;
-        const uint32_t m = (((ok >> v_page) & 1) && key0 + key < kv_len) ? ~0u : 0u;
-        vreg[e].x &= m; vreg[e].y &= m; vreg[e].z &= m; vreg[e].w &= m;
-      }
+    for (int u = 0; u < 4; ++u) {
+      const int valid = ((p.ok >> u) & 1) ? max(0, min(kPage, kv_len - tile * kKeys - u * kPage)) : 0;
+      const uint64_t blk = reinterpret_cast<uint64_t>(block_at(vbase, id[u]));
+      const i32x4_t rsrc = {__builtin_amdgcn_readfirstlane(int(uint32_t(blk))),
+                            __builtin_amdgcn_readfirstlane(int(uint32_t(blk >> 32) & 0xFFFF)),
+                            __builtin_amdgcn_readfirstlane(int(uint32_t(valid) * uint32_t(tok_bytes))),
+                            kBufferRsrcWord3};
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                   :: "s"(lds_addr(buf.b + (u * kPage + 4 * wave) * kKRow)), "v"(v_lane_off),
+                      "s"(rsrc) : "memory");
     }
+  };
+
+  uint32_t v_rd[4];
+  {
+    const int e = (lane >> 2) & 3, q = lane & 3, gp = (lane >> 4) & 1, hh = lane >> 5;
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      *reinterpret_cast<uint4*>(buf.k + (u * kPage + k_tok) * kKPitch + k_chunk * 16) = kreg[u];
-    // V: 8 dims x 4 keys written transposed.
-    const uint32_t w[4][4] = {{vreg[0].x, vreg[0].y, vreg[0].z, vreg[0].w},
-                              {vreg[1].x, vreg[1].y, vreg[1].z, vreg[1].w},
-                              {vreg[2].x, vreg[2].y, vreg[2].z, vreg[2].w},
-                              {vreg[3].x, vreg[3].y, vreg[3].z, vreg[3].w}};
-    const int key = v_page * kPage + v_tok;
-    uint8_t* dst = buf.vt + (v_chunk * 8) * kVPitch + vt_pos(key) * 2;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      // dims 2c (low halves) and 2c+1 (high halves) of the chunk
-      const uint32_t lo01 = __builtin_amdgcn_perm(w[1][c], w[0][c], 0x05040100u);
-      const uint32_t lo23 = __builtin_amdgcn_perm(w[3][c], w[2][c], 0x05040100u);
-      const uint32_t hi01 = __builtin_amdgcn_perm(w[1][c], w[0][c], 0x07060302u);
-      const uint32_t hi23 = __builtin_amdgcn_perm(w[3][c], w[2][c], 0x07060302u);
-      *reinterpret_cast<uint2*>(dst + (2 * c) * kVPitch) = make_uint2(lo01, lo23);
-      *reinterpret_cast<uint2*>(dst + (2 * c + 1) * kVPitch) = make_uint2(hi01, hi23);
-    }
+    for (int db = 0; db < 4; ++db)
+      v_rd[db] = (4 * hh + e) * kKRow + ((4 * (db ^ e) + 2 * gp + (q >> 1)) << 4) + ((q & 1) << 3);
+  }
+  // MFMA operands from LDS.  Score MFMA i (0..15) of a tile: k-step i/2 of
+  // key block i%2 (keys 32(i%2) .. +31), A = those keys' dims.  Output MFMA
+  // i: key step i/4 (keys 16(i/4) .. +15), head-dim block i%4, A = V^T rows.
+  auto k_operand = [&](const KTile& buf, int i) __attribute__((always_inline)) {
+    return as_bf16x8(*reinterpret_cast<const uint4*>(
+        buf.b + (32 * (i & 1) + r) * kKRow + (((2 * (i >> 1) + half) ^ (r & 15)) << 4)));
+  };
+  // The V^T operand comes from the [key][dim] tile through two transposing
+  // reads (ds_read_b64_tr_b16).  Within a group of 16 lanes, lane j supplies
+  // the address of 4 consecutive elements and lane i receives element i%4 of
+  // the rows supplied by lanes i/4 + {0,4,8,12}.  So lane j = 4e + q of
+  // group g points at key 16st + 4(g/2) + e (+8 for the second read), dims
+  // 32db + 16(g%2) + 4q .. +3, and lane i of the group receives dim
+  // 32db + 16(g%2) + i for the four keys -- the rows and key order of the
+  // P^T operand.  v_rd[db]: this lane's address for k-step 0.
+  auto v_operand = [&](const VTile& buf, int i) __attribute__((always_inline)) {
+    const uint8_t* p = buf.b + v_rd[i & 3] + (i >> 2) * 16 * kKRow;
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + 8 * kKRow));
+    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
 
   f32x16_t o[4];
@@ -249,89 +290,91 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[db][e] = 0.f;
-  float m_run = kNegBig, l_run = 0.f;
+  // m_run: the row's running max (base 2, scaled); l_half: the running sum
+  // of p over this lane's half of every tile's keys (lane l^32 holds the
+  // other half), both under the same m_run.
+  float m_run = kNegBig, l_half = 0.f;
+  const uint32_t ones = 0x3F803F80u;  // bf16 pair (1, 1)
 
   // Accumulator entry e of key block kb holds key 32kb + 8(e/4) + 4half + e%4
   // of the tile, which lies in page 2kb + e/8 of the tile.  Interior tiles
   // (every key visible to every row of the workgroup, all pages present)
-  // skip the per-key tests: compute<false>.
-  auto compute = [&](const TileBuf& buf, int tile, int ok, auto masked) __attribute__((always_inline)) {
-    constexpr bool kMasked = decltype(masked)::value;
-    // S^T for key blocks 0 and 1 (keys 32kb .. 32kb+31 of the tile).
-    f32x16_t s[2];
+  // skip the per-key tests: masked = false.  rel = the key offset (within
+  // the lane's half of the tile) the row may still see.
+  auto visible = [&](int rel, int ok, int kb, int e, auto masked) __attribute__((always_inline)) {
+    if constexpr (decltype(masked)::value)
+      return (32 * kb + 8 * (e >> 2) + (e & 3)) <= rel && ((ok >> (2 * kb + (e >> 3))) & 1);
+    else
+      return true;
+  };
+  auto rel_of = [&](int tile) __attribute__((always_inline)) {
+    return limit - tile * kKeys - 4 * half;
+  };
+  // Max of the raw scores of quarter q (key block q/2, entries 8(q%2) .. +7).
+  auto quarter_max = [&](const f32x16_t (&s)[2], int q, int rel, int ok, float mx, auto masked)
+      __attribute__((always_inline)) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
-      const uint8_t* krow = buf.k + (32 * kb + r) * kKPitch + 16 * half;
-#pragma unroll
-      for (int ks = 0; ks < kD / 16; ++ks) {
-        const bf16x8_t ka = as_bf16x8(*reinterpret_cast<const uint4*>(krow + 32 * ks));
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qb[ks], s[kb], 0, 0, 0);
-      }
-    }
-    // Key offset (within the lane's half of the tile) this row may still see.
-    const int rel = limit - tile * kKeys - 4 * half;
-    auto visible = [&](int kb, int e) __attribute__((always_inline)) {
-      if constexpr (kMasked)
-        return (32 * kb + 8 * (e >> 2) + (e & 3)) <= rel && ((ok >> (2 * kb + (e >> 3))) & 1);
-      else
-        return true;
-    };
-    // Row max of the raw scores (the scale is positive), over this lane's 32
-    // keys and lane l^32's.
-    float mx = kNegBig;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        if (visible(kb, e)) mx = fmaxf(mx, s[kb][e]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    // The running max only moves when some row's max grew by more than
-    // kRescaleLog2 (base-2 units); otherwise the stale max stays, p <= 2^8,
-    // and the O rescale is skipped -- same result, 64 fewer multiplies.
+    for (int e = 8 * (q & 1); e < 8 * (q & 1) + 8; ++e)
+      if (visible(rel, ok, q >> 1, e, masked)) mx = fmaxf(mx, s[q >> 1][e]);
+    return mx;
+  };
+  // Folds a tile's row max (this lane's 32 keys and lane l^32's; the raw
+  // scores, as the scale is positive) into the running max.  A row's running
+  // max only moves when its max grew by more than kRescaleLog2 (base-2
+  // units); otherwise the stale max stays, p <= 2^8, and the rescale of O and
+  // l is skipped -- same result, 65 fewer multiplies.
+  auto fold_max = [&](float mx) __attribute__((always_inline)) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                     false, false);
+    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    // Each row decides for itself (the branch is only skipped when no row of
+    // the wave needs it), so a row's result does not depend on which other
+    // rows share its wave.
     const float cand = fmaxf(m_run, mx * a.scale_log2);
-    if (__builtin_amdgcn_ballot_w64(cand > m_run + kRescaleLog2) != 0) {
-      const float alpha = fast_exp2(m_run - cand);
-      m_run = cand;
-      l_run *= alpha;
+    const bool grow = cand > m_run + kRescaleLog2;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float alpha = grow ? fast_exp2(m_run - cand) : 1.f;
+      m_run = grow ? cand : m_run;
+      l_half *= alpha;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
     }
-    float sum = 0.f;
-    uint32_t pw[2][8];  // P as bf16 pairs, in S^T accumulator order
+  };
+  // Exponent pair i (0..15) of a tile: p = exp2(S scale - m_run) for entries
+  // 2(i%8), +1 of key block i/8, packed to a bf16 pair in S^T accumulator
+  // order and added (as rounded) into `sum`.
+  auto exp_pair = [&](const f32x16_t (&s)[2], int i, int rel, int ok, auto masked,
+                      uint32_t (&pw)[2][8], float& sum) __attribute__((always_inline)) {
+    const int kb = i >> 3, e = 2 * (i & 7);
+    const float p0 = visible(rel, ok, kb, e, masked)
+                         ? fast_exp2(fmaf(s[kb][e], a.scale_log2, -m_run)) : 0.f;
+    const float p1 = visible(rel, ok, kb, e + 1, masked)
+                         ? fast_exp2(fmaf(s[kb][e + 1], a.scale_log2, -m_run)) : 0.f;
+    pw[kb][e >> 1] = pack_bf16(p0, p1);
+    sum = dot2_bf16(pw[kb][e >> 1], ones, sum);
+  };
+  // The 16 score MFMAs of a tile, alone (first tile).
+  auto scores = [&](const KTile& buf, f32x16_t (&s)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int e = 0; e < 16; e += 2) {
-        const float p0 = visible(kb, e) ? fast_exp2(fmaf(s[kb][e], a.scale_log2, -m_run)) : 0.f;
-        const float p1 =
-            visible(kb, e + 1) ? fast_exp2(fmaf(s[kb][e + 1], a.scale_log2, -m_run)) : 0.f;
-        sum += p0 + p1;
-        pw[kb][e >> 1] = pack_bf16(p0, p1);
-      }
-    sum += __shfl_xor(sum, 32);
-    l_run += sum;
-    // O^T += V^T P^T, k-step st = keys 16st .. 16st+15 of the tile, whose
-    // P^T operand is accumulator entries 8(st%2) .. +7 of key block st/2.
+      for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
 #pragma unroll
-    for (int st = 0; st < kKeys / 16; ++st) {
-      const uint32_t* pp = &pw[st >> 1][4 * (st & 1)];
-      const bf16x8_t pb = as_bf16x8(make_uint4(pp[0], pp[1], pp[2], pp[3]));
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const bf16x8_t va = as_bf16x8(*reinterpret_cast<const uint4*>(
-            buf.vt + (32 * db + r) * kVPitch + (16 * st + 8 * half) * 2));
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[db], 0, 0, 0);
-      }
-    }
+    for (int i = 0; i < 16; ++i)
+      s[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_operand(buf, i), qb[i >> 1], s[i & 1],
+                                                         0, 0, 0);
   };
 
   // Tiles [0, n_full) are interior for every row of the workgroup: all its
   // rows see keys up to at least lim_lo (its first token's limit), and a
   // first pass checks that every page the item visits exists.
+  // V tiles start as zeros: should a bounded load leave the LDS rows of
+  // out-of-range lanes untouched, they hold zeros or earlier valid rows,
+  // never stale bits from before the kernel.
+  for (int o16 = threadIdx.x; o16 < int(2 * sizeof(VTile) / 16); o16 += kThreads)
+    reinterpret_cast<uint4*>(vtiles[0].b)[o16] = make_uint4(0, 0, 0, 0);
   int bad = 0;
   const int pages_used = min(npages, ntiles * 4);
   for (int p = threadIdx.x; p < pages_used; p += kThreads) {
@@ -342,33 +385,135 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   const bool all_pages = __syncthreads_and(bad == 0);
   const int lim_lo = a.causal ? tok0 + kv_len - q_len : kv_len - 1;
   const int n_full = all_pages ? max(0, min(ntiles, (lim_lo + 1) / kKeys)) : 0;
-  // Per iteration: K/V loads of tile+1 (ids fetched last iteration), id
-  // fetch of tile+2, the tile's math, staging of tile+1, one barrier.
-  TileIds ids_next;
-  auto run_tiles = [&](int t0, int t1, int ok, auto masked) __attribute__((always_inline)) {
-    for (int tile = t0; tile < t1; ++tile) {
-      int next_ok = 0;
-      if (tile + 1 < ntiles) {
-        next_ok = load_tile(ids_next);
-        if (tile + 2 < ntiles) ids_next = fetch_ids(tile + 2);
+
+  // Step j.  On entry: s_cur = raw S^T of tile j, already folded into
+  // m_run; K of tile j+1 staged in ktiles[(j+1)&1] and V of tile j in
+  // vtiles[j&1]; pages_v = pages of tile j+1; raw_k = page ids of tile j+2
+  // (in flight).  A wave issues in order and an MFMA occupies the matrix
+  // pipe for 32 cycles, so the step interleaves, in program order (fenced
+  // with sched_barrier):
+  //   1. the 16 score MFMAs of tile j+1 with the exponentials of tile j,
+  //      one exponent pair per MFMA;
+  //   2. the 16 MFMAs of O^T += V^T P^T for tile j with the row max of tile
+  //      j+1 and the staging of K of tile j+2 and V of tile j+1 (loaded into
+  //      registers at the start of the step, written into the buffers step
+  //      j-1 read);
+  // each with its LDS operand read three MFMAs ahead; then it folds the row
+  // max into m_run and ends on the barrier.  mc / mn: whether tiles j / j+1
+  // need the per-key tests.
+  f32x16_t s_cur[2];
+  int ok_cur = 0;
+  Pages pages_v{0, 0, 0, 0, 0};
+  RawIds raw_k{};
+  auto step = [&](int j, auto mc, auto mn, auto has_next) __attribute__((always_inline)) {
+    constexpr bool kNext = decltype(has_next)::value;
+    // The ids of tile j+2 (loaded last step) are read before this step
+    // issues any load.
+    const bool k2 = j + 2 < ntiles;
+    const Pages pages_k = resolve(raw_k, j + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    if (k2) dma_k(ktiles[j & 1], pages_k);
+    if constexpr (kNext) dma_v(vtiles[(j + 1) & 1], pages_v, j + 1);
+    if (j + 3 < ntiles) raw_k = fetch_ids(j + 3);
+
+    // 1. scores of tile j+1 beside the exponentials of tile j.
+    uint32_t pw[2][8];
+    f32x16_t s_nxt[2];
+    {
+      const int rel = rel_of(j);
+      float sum0 = 0.f, sum1 = 0.f;
+      if constexpr (kNext) {
+        const KTile& kb = ktiles[(j + 1) & 1];
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) s_nxt[q][e] = 0.f;
+        bf16x8_t kop[16];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) kop[i] = k_operand(kb, i);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (i + 3 < 16) kop[i + 3] = k_operand(kb, i + 3);
+          s_nxt[i & 1] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[i], qb[i >> 1], s_nxt[i & 1], 0, 0, 0);
+          exp_pair(s_cur, i, rel, ok_cur, mc, pw, (i & 1) ? sum1 : sum0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) exp_pair(s_cur, i, rel, ok_cur, mc, pw, (i & 1) ? sum1 : sum0);
       }
-      compute(tiles[tile & 1], tile, ok, masked);
-      if (tile + 1 < ntiles) stage_tile(tiles[(tile + 1) & 1], tile + 1, next_ok);
-      ok = next_ok;
-      __syncthreads();
+      l_half += sum0 + sum1;
     }
-    return ok;
+
+    // 2. P_j V_j beside the row max of tile j+1 and the staging.
+    {
+      const VTile& vb = vtiles[j & 1];
+      const int rel = rel_of(j + 1);
+      float mx = kNegBig;
+      bf16x8_t vop[16];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) vop[i] = v_operand(vb, i);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (i + 3 < 16) vop[i + 3] = v_operand(vb, i + 3);
+        const int st = i >> 2;
+        const uint32_t* pp = &pw[st >> 1][4 * (st & 1)];
+        const bf16x8_t pb = as_bf16x8(make_uint4(pp[0], pp[1], pp[2], pp[3]));
+        o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[i], pb, o[i & 3], 0, 0, 0);
+        if constexpr (kNext) {
+          if (i < 4) mx = quarter_max(s_nxt, i, rel, pages_v.ok, mx, mn);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (kNext) fold_max(mx);
+    }
+    wait_dma();
+    __syncthreads();
+    if constexpr (kNext) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) s_cur[q] = s_nxt[q];
+      ok_cur = pages_v.ok;
+      pages_v = pages_k;
+    }
   };
   if (ntiles > 0) {
-    int ok = load_tile(fetch_ids(0));
-    if (ntiles > 1) ids_next = fetch_ids(1);
-    stage_tile(tiles[0], 0, ok);
+    const Pages p0 = resolve(fetch_ids(0), 0);
+    dma_k(ktiles[0], p0);
+    dma_v(vtiles[0], p0, 0);
+    RawIds raw1{};
+    if (ntiles > 1) raw1 = fetch_ids(1);
+    if (ntiles > 1) {
+      pages_v = resolve(raw1, 1);
+      dma_k(ktiles[1], pages_v);
+    }
+    if (ntiles > 2) raw_k = fetch_ids(2);
+    wait_dma();
     __syncthreads();
-    ok = run_tiles(0, n_full, ok, std::false_type{});
-    run_tiles(n_full, ntiles, ok, std::true_type{});
+    scores(ktiles[0], s_cur);
+    ok_cur = p0.ok;
+    {
+      const int rel = rel_of(0);
+      float mx = kNegBig;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) mx = quarter_max(s_cur, q, rel, ok_cur, mx, std::true_type{});
+      fold_max(mx);
+    }
+    __syncthreads();  // every wave has read ktiles[0] before step 0 refills it
+    const int last = ntiles - 1;
+    int j = 0;
+    for (; j + 1 < min(n_full, ntiles); ++j)
+      step(j, std::false_type{}, std::false_type{}, std::true_type{});
+    if (j < n_full && j < last) {
+      step(j, std::false_type{}, std::true_type{}, std::true_type{});
+      ++j;
+    }
+    for (; j < last; ++j) step(j, std::true_type{}, std::true_type{}, std::true_type{});
+    step(last, std::true_type{}, std::true_type{}, std::false_type{});
   }
 
   if (!row_ok) return;
+  const float l_run = l_half + __shfl_xor(l_half, 32);
   // O^T column r = this row; entry (db, 4i+j) = head dim 32db + 8i + 4half + j.
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
   uint16_t* dst = a.out + int64_t(q_off + tok) * a.out_stride + int64_t(hq) * kD + 4 * half;
@@ -486,6 +631,8 @@ extern "C" int kvc_batch_prefill_run(const kvc_prefill_schedule* sched, const in
               KVC_ERR_INVALID_ARG, "cache strides smaller than the block");
   KVC_REQUIRE(cache_token_stride * kPage * 2 < (int64_t(1) << 31), KVC_ERR_INVALID_ARG,
               "a cache block spans more than 2 GiB");
+  KVC_REQUIRE(cache_block_stride * 2 < (int64_t(1) << 32), KVC_ERR_INVALID_ARG,
+              "cache blocks 4 GiB or more apart");
   KVC_REQUIRE(q_token_stride >= int64_t(Hq) * kD && out_token_stride >= int64_t(Hq) * kD,
               KVC_ERR_INVALID_ARG, "q/out token stride smaller than Hq*head_dim");
   KVC_REQUIRE(sm_scale > 0.f, KVC_ERR_INVALID_ARG, "sm_scale must be positive");
