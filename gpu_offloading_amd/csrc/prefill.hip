@@ -69,6 +69,8 @@ constexpr int kBufferRsrcWord3 = 0x00020000;
 // s_waitcnt vmcnt(0) with the other counters unconstrained (gfx9 encoding:
 // vmcnt [3:0],[15:14]; expcnt [6:4]; lgkmcnt [11:8]).
 constexpr int kWaitVmcnt0 = 0x0F70;
+// s_waitcnt lgkmcnt(0) with the other counters unconstrained.
+constexpr int kWaitLgkmcnt0 = 0xC07F;
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kLog2e = 1.44269504088896340736f;
 
@@ -181,8 +183,15 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   struct RawIds { int32_t v[4]; };
   auto fetch_ids = [&](int tile) __attribute__((always_inline)) {
     RawIds t;
+    const int b = page_off + tile * 4;
+    if (b + 3 <= last_index) {
+      const int32_t* q = a.indices + b;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) t.v[u] = a.indices[min(page_off + tile * 4 + u, last_index)];
+      for (int u = 0; u < 4; ++u) t.v[u] = q[u];
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) t.v[u] = a.indices[min(b + u, last_index)];
+    }
     return t;
   };
   // Wave-uniform page ids of a tile; bit u of `ok` says page u is real
@@ -190,14 +199,17 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   // masked.  (Plain scalars, not an array: a copy carried across steps must
   // stay in registers.)
   struct Pages { int32_t id0, id1, id2, id3; int ok; };
+  // Pages [0, pages_here) of the item exist in the request and the index
+  // array; a present page also needs an id in [0, num_blocks).  (Bitwise
+  // tests, no short-circuit branches.)
+  const int pages_here = min(npages, last_index - page_off + 1);
   auto resolve = [&](const RawIds& t, int tile) __attribute__((always_inline)) {
     int32_t id[4];
     int ok = 0;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int32_t v = __builtin_amdgcn_readfirstlane(t.v[u]);
-      const int p = tile * 4 + u;
-      const bool good = p < npages && page_off + p <= last_index && v >= 0 && v < num_blocks32;
+      const bool good = (tile * 4 + u < pages_here) & (uint32_t(v) < uint32_t(num_blocks32));
       ok |= good ? (1 << u) : 0;
       id[u] = good ? v : 0;
     }
@@ -240,21 +252,54 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   // no such care: a key's score depends on its own K row only, and tiles
   // holding such keys are processed with the per-key tests, which never
   // read its score.
-  auto dma_v = [&](VTile& buf, const Pages& p, int tile) __attribute__((always_inline)) {
+  auto dma_v_pages = [&](VTile& buf, const Pages& p, const int (&bytes)[4]) __attribute__((always_inline)) {
     const int32_t id[4] = {p.id0, p.id1, p.id2, p.id3};
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int valid = ((p.ok >> u) & 1) ? max(0, min(kPage, kv_len - tile * kKeys - u * kPage)) : 0;
       const uint64_t blk = reinterpret_cast<uint64_t>(block_at(vbase, id[u]));
       const i32x4_t rsrc = {__builtin_amdgcn_readfirstlane(int(uint32_t(blk))),
                             __builtin_amdgcn_readfirstlane(int(uint32_t(blk >> 32) & 0xFFFF)),
-                            __builtin_amdgcn_readfirstlane(int(uint32_t(valid) * uint32_t(tok_bytes))),
-                            kBufferRsrcWord3};
+                            __builtin_amdgcn_readfirstlane(bytes[u]), kBufferRsrcWord3};
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                    :: "s"(lds_addr(buf.b + (u * kPage + 4 * wave) * kKRow)), "v"(v_lane_off),
                       "s"(rsrc) : "memory");
     }
   };
+  // Bytes of each page's valid tokens: all 16 on a tile inside the cache
+  // (every tile but a request's last), fewer in the page holding kv_len,
+  // none in a missing page.
+  const int page_bytes = kPage * int(tok_bytes);  // under 2 GiB (host check)
+  auto dma_v = [&](VTile& buf, const Pages& p, int tile) __attribute__((always_inline)) {
+    if ((tile + 1) * kKeys <= kv_len) {
+      const int bytes[4] = {(p.ok & 1) ? page_bytes : 0, (p.ok & 2) ? page_bytes : 0,
+                            (p.ok & 4) ? page_bytes : 0, (p.ok & 8) ? page_bytes : 0};
+      dma_v_pages(buf, p, bytes);
+    } else {
+      int bytes[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int rem = max(0, min(kPage, kv_len - tile * kKeys - u * kPage));
+        bytes[u] = ((p.ok >> u) & 1) ? rem * int(tok_bytes) : 0;
+      }
+      dma_v_pages(buf, p, bytes);
+    }
+  };
+
+  // The first tiles' page ids are fetched now, beside the Q loads.
+  const RawIds raw0 = fetch_ids(0);
+  RawIds raw1{};
+  if (ntiles > 1) raw1 = fetch_ids(1);
+  // V tiles start as zeros: should a bounded load leave the LDS rows of
+  // out-of-range lanes untouched, they hold zeros or earlier valid rows,
+  // never stale bits from before the kernel.  Each wave clears the rows its
+  // own loads fill (rows 16u + 4*wave .. +3 of both buffers) and waits for
+  // that before issuing them.
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    uint8_t* row = vtiles[c >> 2].b + ((c & 3) * kPage + 4 * wave + (lane >> 4)) * kKRow;
+    *reinterpret_cast<uint4*>(row + (lane & 15) * 16) = make_uint4(0, 0, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitLgkmcnt0);
 
   uint32_t v_rd[4];
   {
@@ -367,24 +412,11 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
                                                          0, 0, 0);
   };
 
-  // Tiles [0, n_full) are interior for every row of the workgroup: all its
-  // rows see keys up to at least lim_lo (its first token's limit), and a
-  // first pass checks that every page the item visits exists.
-  // V tiles start as zeros: should a bounded load leave the LDS rows of
-  // out-of-range lanes untouched, they hold zeros or earlier valid rows,
-  // never stale bits from before the kernel.
-  for (int o16 = threadIdx.x; o16 < int(2 * sizeof(VTile) / 16); o16 += kThreads)
-    reinterpret_cast<uint4*>(vtiles[0].b)[o16] = make_uint4(0, 0, 0, 0);
-  int bad = 0;
-  const int pages_used = min(npages, ntiles * 4);
-  for (int p = threadIdx.x; p < pages_used; p += kThreads) {
-    const int64_t at = int64_t(page_off) + p;
-    const int32_t id = at < a.num_indices ? a.indices[at] : -1;
-    bad |= id < 0 || id >= a.num_blocks;
-  }
-  const bool all_pages = __syncthreads_and(bad == 0);
+  // Tiles [0, n_full) are interior for every row of the workgroup when all
+  // their pages are present: all its rows see keys up to at least lim_lo
+  // (its first token's limit).
   const int lim_lo = a.causal ? tok0 + kv_len - q_len : kv_len - 1;
-  const int n_full = all_pages ? max(0, min(ntiles, (lim_lo + 1) / kKeys)) : 0;
+  const int n_full = max(0, min(ntiles, (lim_lo + 1) / kKeys));
 
   // Step j.  On entry: s_cur = raw S^T of tile j, already folded into
   // m_run; K of tile j+1 staged in ktiles[(j+1)&1] and V of tile j in
@@ -478,11 +510,9 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
     }
   };
   if (ntiles > 0) {
-    const Pages p0 = resolve(fetch_ids(0), 0);
+    const Pages p0 = resolve(raw0, 0);
     dma_k(ktiles[0], p0);
     dma_v(vtiles[0], p0, 0);
-    RawIds raw1{};
-    if (ntiles > 1) raw1 = fetch_ids(1);
     if (ntiles > 1) {
       pages_v = resolve(raw1, 1);
       dma_k(ktiles[1], pages_v);
@@ -500,16 +530,17 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
       fold_max(mx);
     }
     __syncthreads();  // every wave has read ktiles[0] before step 0 refills it
+    using F = std::false_type;
+    using T = std::true_type;
+    // Interior steps while tiles j and j+1 are interior and their pages all
+    // present, then one step into the masked tiles, then masked steps (a
+    // missing page, an error case, sends the rest down the masked path).
     const int last = ntiles - 1;
     int j = 0;
-    for (; j + 1 < min(n_full, ntiles); ++j)
-      step(j, std::false_type{}, std::false_type{}, std::true_type{});
-    if (j < n_full && j < last) {
-      step(j, std::false_type{}, std::true_type{}, std::true_type{});
-      ++j;
-    }
-    for (; j < last; ++j) step(j, std::true_type{}, std::true_type{}, std::true_type{});
-    step(last, std::true_type{}, std::true_type{}, std::false_type{});
+    for (; j + 1 < n_full && (ok_cur & pages_v.ok) == 0xF; ++j) step(j, F{}, F{}, T{});
+    if (j < n_full && j < last && ok_cur == 0xF) step(j++, F{}, T{}, T{});
+    for (; j < last; ++j) step(j, T{}, T{}, T{});
+    step(last, T{}, T{}, F{});
   }
 
   if (!row_ok) return;
