@@ -13,13 +13,14 @@
 //
 // Schedule (balanced split-KV, computed on the host by kvc_decode_plan like
 // FlashInfer's plan()): the flattened page list indices[0 .. P) of the whole
-// batch is cut into S segments of equal length, S ~ the number of workgroups
-// the GPU holds at once, so every workgroup streams the same number of pages
-// and all finish together whatever the spread of request lengths.  A segment
-// crosses request boundaries; the part of a request inside one segment is a
-// "piece".  A request covered by one piece is written straight to the output;
-// otherwise each piece leaves an fp32 partial + log2-sum-exp in the workspace
-// and decode_merge_kernel folds them.
+// batch is cut into S segments of equal cost, S ~ the number of workgroups
+// the GPU holds at once, so every workgroup streams about the same number of
+// pages and all finish together whatever the spread of request lengths (a
+// switch to another request inside a segment costs about one page more; see
+// cut_segments).  A segment crosses request boundaries; the part of a request
+// inside one segment is a "piece".  A request covered by one piece is written
+// straight to the output; otherwise each piece leaves an fp32 partial +
+// log2-sum-exp in the workspace and decode_merge_kernel folds them.
 //
 // head_dim 128 (the reference models) uses decode_lds_kernel<G, HPW>: grid
 // (S, Hkv / HPW), one wave per KV head, HPW = 8 heads per workgroup when the
@@ -41,9 +42,7 @@
 // Softmax statistics live per 16-lane DPP row (one query head per row).
 // A wave's page ids are loaded once, one per lane (2 registers: up to 128
 // pages per segment), and broadcast with v_readlane, so no dependent global
-// load sits in the streaming loop.  A workgroup derives its span of the page
-// list from its segment index, so the id loads and the segment/piece record
-// loads go out together at kernel start.
+// load sits in the streaming loop.
 //
 // head_dim 64 and 256 use decode_reg_kernel: grid (S, ceil(Hkv / 4)), one
 // wave per KV head, no barrier; K/V stay in registers: lane (row r, column c)
@@ -54,6 +53,7 @@
 #include <algorithm>
 #include <cmath>
 #include <mutex>
+#include <vector>
 
 namespace kvc {
 namespace {
@@ -112,13 +112,11 @@ __device__ __forceinline__ void wave_lds_fence() {
 }
 
 
-// First slot and page count of segment s.  The plan cuts the flattened page
-// list into equal parts, so both follow from the segment index, and a
-// workgroup can fetch its page ids without waiting for its segment record.
-__device__ __forceinline__ void segment_span(const DecodeArgs& a, int s, int& g0, int& n) {
-  const int64_t t = a.total_pages;
-  g0 = int(int64_t(s) * t / a.num_segments);
-  n = min(int(int64_t(s + 1) * t / a.num_segments) - g0, kMaxSegPages);
+// First slot and page count of a segment, from its record (the plan's cuts
+// balance pages and piece switches, so they do not follow from the index).
+__device__ __forceinline__ void segment_span(const int4& segment, int& g0, int& n) {
+  g0 = segment.z;
+  n = min(segment.w, kMaxSegPages);
 }
 
 // Page ids of a segment: lane l of register r holds indices[g0 + l + 64 r].
@@ -252,7 +250,7 @@ __global__ __launch_bounds__(64 * HPW) void decode_lds_kernel(DecodeArgs a) {
   const int h = h0 + wave;
   const int4 segment = a.segments[blockIdx.x];
   int g0, n;
-  segment_span(a, blockIdx.x, g0, n);
+  segment_span(segment, g0, n);
   int k = segment.x;
   const int k_end = segment.y;
   if (k >= k_end || n <= 0) return;  // uniform over the workgroup
@@ -874,7 +872,7 @@ __global__ __launch_bounds__(kThreads) void decode_reg_kernel(DecodeArgs a) {
   if (h >= a.num_kv_heads) return;
   const int4 segment = a.segments[blockIdx.x];
   int g0, n;
-  segment_span(a, blockIdx.x, g0, n);
+  segment_span(segment, g0, n);
   int k = segment.x;
   const int k_end = segment.y;
   if (k >= k_end || n <= 0) return;
@@ -1083,6 +1081,47 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(MergeArgs a) {
   if (a.lse && lane == 0) a.lse[int64_t(b) * Hq + hq] = (mx + fast_log2(S)) * kLn2;
 }
 
+// Segment cuts of the flattened page list [0, total): cut[s] is segment s's
+// first page, cut[segs] = total.  The segments cost the same, a page counting
+// kPageCost and every request that starts strictly inside a segment
+// kSwitchCost more: at such a piece switch the workgroup loads the next
+// request's record and q while its page pipeline drains by about one page
+// (a 35-page segment with one switch was measured 2.5 us = 1.15 pages slower
+// than one without).  Every segment keeps at least one page; if the balanced
+// cuts would give a segment more than kMaxSegPages pages, equal page counts
+// are used instead.
+constexpr int64_t kPageCost = 8;
+constexpr int64_t kSwitchCost = 9;
+
+std::vector<int64_t> cut_segments(const int32_t* indptr, int batch, int64_t total,
+                                  int64_t segs) {
+  std::vector<int64_t> cut(size_t(segs) + 1);
+  cut[0] = 0;
+  cut[size_t(segs)] = total;
+  if (segs <= 1) return cut;
+  // first pages of the requests after the first non-empty one
+  std::vector<int64_t> starts;
+  for (int b = 1; b < batch; ++b)
+    if (indptr[b + 1] > indptr[b] && indptr[b] > 0) starts.push_back(indptr[b]);
+  const __int128 T = __int128(kPageCost) * total + __int128(kSwitchCost) * int64_t(starts.size());
+  int64_t x = 0, below = 0;  // below = starts < x
+  size_t next = 0;
+  bool ok = true;
+  for (int64_t s = 1; s < segs; ++s) {
+    const __int128 target = __int128(s) * T / segs;
+    while (x < total && __int128(kPageCost) * x + __int128(kSwitchCost) * below < target) {
+      ++x;
+      while (next < starts.size() && starts[next] < x) ++below, ++next;
+    }
+    cut[size_t(s)] = std::min(std::max(x, cut[size_t(s) - 1] + 1), total - (segs - s));
+    ok = ok && cut[size_t(s)] - cut[size_t(s) - 1] <= kMaxSegPages;
+  }
+  ok = ok && total - cut[size_t(segs) - 1] <= kMaxSegPages;
+  if (!ok)
+    for (int64_t s = 1; s < segs; ++s) cut[size_t(s)] = s * total / segs;
+  return cut;
+}
+
 // KV heads per workgroup of the streaming kernel: 8 (one block-row slice of
 // 2 KB per token) for the head_dim-128 kernel when the heads divide evenly
 // and the register budget allows two waves per SIMD, else one; the register
@@ -1231,8 +1270,10 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, const int32_t* last_p
   }
   KVC_REQUIRE(segs <= (int64_t(1) << 30), KVC_ERR_INVALID_ARG, "too many segments");
 
+  const std::vector<int64_t> cut = cut_segments(indptr_host, batch, total, segs);
+
   // Small batches (head_dim 128, no forced segment count): when every request
-  // fits in kSmallMaxPages pages and the equal segments would cut a request,
+  // fits in kSmallMaxPages pages and the segments would cut a request,
   // one workgroup per (request, KV head) streams it and merges its waves'
   // states in LDS instead (no partials, no merge launch).
   int64_t max_pages = 0;
@@ -1240,7 +1281,7 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, const int32_t* last_p
     max_pages = std::max<int64_t>(max_pages, indptr_host[b + 1] - indptr_host[b]);
   bool splits = false;
   for (int64_t s = 1, bb = 0; s < segs && !splits; ++s) {
-    const int64_t g = s * total / segs;  // first page of segment s
+    const int64_t g = cut[size_t(s)];  // first page of segment s
     while (bb < batch && indptr_host[bb + 1] <= g) ++bb;
     splits = bb < batch && indptr_host[bb] < g;  // pages g-1 and g in request bb
   }
@@ -1318,8 +1359,8 @@ extern "C" int kvc_decode_plan(const int32_t* indptr_host, const int32_t* last_p
   int b = 0;
   int32_t append_pieces = 0;
   for (int64_t s = 0; s < segs; ++s) {
-    const int64_t g0 = s * total / segs;
-    const int64_t g1 = (s + 1) * total / segs;
+    const int64_t g0 = cut[size_t(s)];
+    const int64_t g1 = cut[size_t(s) + 1];
     int32_t* rec = segments + 4 * s;
     rec[0] = int32_t(np);
     rec[2] = int32_t(g0);

@@ -107,9 +107,10 @@ int kvc_gather_kv(
  *
  * kvc_decode_plan is host-only (no device access), like FlashInfer plan(),
  * which also reads a host indptr.  It cuts the batch's flattened page list
- * into num_segments equal segments per group of heads_per_group KV heads (by
+ * into num_segments segments per group of heads_per_group KV heads (by
  * default one per workgroup the GPU holds at once; num_segments_hint > 0
- * forces the count) and writes the plan image into plan_host:
+ * forces the count), balanced in pages plus switches between requests (at
+ * most 128 pages each), and writes the plan image into plan_host:
  *   [0, 4*num_segments)          (first piece, end piece, first slot, pages)
  *   [pieces_offset, +8*pieces)   (request, first slot, end slot, partial or -1,
  *                                 request's last slot, its tokens, 0, 0)

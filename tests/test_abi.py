@@ -98,11 +98,21 @@ def _check_small_plan_image(indptr, sched, img, lpl):
     assert pages.max() <= 16
 
 
+def _segment_costs(indptr, segs):
+    """Planner cost of each segment [g0, g1): 8 per page plus 9 per request
+    start in [g0, g1) (the first request's start excluded)."""
+    starts = [int(indptr[b]) for b in range(1, len(indptr) - 1)
+              if indptr[b + 1] > indptr[b] and indptr[b] > 0]
+    return [8 * int(n) + 9 * sum(1 for x in starts if g0 <= x < g0 + n) for _, _, g0, n in segs]
+
+
 def _check_plan_image(indptr, sched, img, lpl):
-    """Segments are contiguous, equal to within one page, at most 128 pages,
-    and their pieces tile every request's pages exactly once, numbered
-    0..n-1 per request (-1 when a request is a single piece), each carrying
-    its request's last slot and last-page length."""
+    """Segments are contiguous, at least one and at most 128 pages, and equal
+    in cost (8 per page, 9 per switch to another request) to within the cost
+    of one step, or equal in pages to within one when balanced costs would
+    exceed 128 pages; their pieces tile every request's pages exactly once,
+    numbered 0..n-1 per request (-1 when a request is a single piece), each
+    carrying its request's last slot and last-page length."""
     if sched.small_batch:
         return _check_small_plan_image(indptr, sched, img, lpl)
     S = sched.num_segments
@@ -119,10 +129,13 @@ def _check_plan_image(indptr, sched, img, lpl):
         ps = pieces[segs[s, 0]:segs[s, 1]]
         assert len(ps) >= 1
         assert (ps[1:, 1] == ps[:-1, 2]).all()                 # contiguous slots
-        assert ps[0, 1] == s * total // S and ps[-1, 2] == (s + 1) * total // S
+        assert ps[0, 1] == (0 if s == 0 else segs[s - 1, 2] + segs[s - 1, 3])
         assert segs[s, 2] == ps[0, 1] and segs[s, 3] == ps[-1, 2] - ps[0, 1]
         lengths.append(ps[-1, 2] - ps[0, 1])
-    assert max(lengths) - min(lengths) <= 1 and max(lengths) <= 128
+    assert segs[-1, 2] + segs[-1, 3] == total
+    assert min(lengths) >= 1 and max(lengths) <= 128
+    costs = _segment_costs(indptr, segs)
+    assert max(costs) - min(costs) < 2 * (8 + 9) or max(lengths) - min(lengths) <= 1
     assert (rec[:, 4] == indptr[rec[:, 0] + 1] - 1).all()
     assert (rec[:, 5] == lpl[rec[:, 0]]).all()
     for b in range(sched.batch):
