@@ -163,62 +163,45 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   const char* kbase = reinterpret_cast<const char*>(a.k_cache);
   const char* vbase = reinterpret_cast<const char*>(a.v_cache);
   const int64_t tok_bytes = a.token_stride * 2;
-  // K (direct to LDS): lane L fetches key 4*wave + L/16 of each page, the
-  // chunk whose swizzled slot is L%16.
-  const int k_key = 4 * wave + (lane >> 4);
-  const uint32_t k_lane_off =
-      uint32_t(k_key * tok_bytes + (head_off + ((lane & 15) ^ (k_key & 15)) * 8) * 2);
-  // V the same way, with its own swizzle.
-  const uint32_t v_lane_off =
-      uint32_t(k_key * tok_bytes + (head_off + ((lane & 15) ^ (4 * (k_key & 3))) * 8) * 2);
+  // K (direct to LDS): wave w loads page w of a tile; its load i fetches
+  // keys 4i .. 4i+3 of the page, lane L key 4i + L/16, the chunk whose
+  // swizzled slot is L%16.  V the same way, with its own swizzle.
+  uint32_t k_lane_off[4], v_lane_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int key = 4 * i + (lane >> 4);
+    k_lane_off[i] = uint32_t(key * tok_bytes + (head_off + ((lane & 15) ^ (key & 15)) * 8) * 2);
+    v_lane_off[i] = uint32_t(key * tok_bytes + (head_off + ((lane & 15) ^ (4 * (key & 3))) * 8) * 2);
+  }
   // Every global_load_lds of this wave has written LDS (vmcnt 0).
   auto wait_dma = []() __attribute__((always_inline)) { __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); };
 
-  // Page ids of a tile as loaded: four independent loads at clamped
-  // addresses, fetched well before their K/V loads need them.  All index
-  // arithmetic is 32-bit so that it stays on the scalar unit (the host keeps
-  // every page index below 2^31).
+  // Page ids of a tile as loaded: lane u (u = lane % 4) loads page u at a
+  // clamped address, one load per tile, fetched well before the K/V loads
+  // need them.  Index arithmetic is 32-bit (the host keeps every page index
+  // below 2^31).
   const int32_t last_index = int32_t(min(a.num_indices - 1, int64_t(INT32_MAX)));
   const int32_t num_blocks32 = int32_t(min(a.num_blocks, int64_t(INT32_MAX)));
-  struct RawIds { int32_t v[4]; };
+  struct RawIds { int32_t v; };
   auto fetch_ids = [&](int tile) __attribute__((always_inline)) {
-    RawIds t;
-    const int b = page_off + tile * 4;
-    if (b + 3 <= last_index) {
-      const int32_t* q = a.indices + b;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) t.v[u] = q[u];
-    } else {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) t.v[u] = a.indices[min(b + u, last_index)];
-    }
-    return t;
+    return RawIds{a.indices[min(page_off + tile * 4 + (lane & 3), last_index)]};
   };
-  // Wave-uniform page ids of a tile; bit u of `ok` says page u is real
-  // (inside the request and the cache), the others read block 0 and are
-  // masked.  (Plain scalars, not an array: a copy carried across steps must
-  // stay in registers.)
-  struct Pages { int32_t id0, id1, id2, id3; int ok; };
+  // Wave-uniform byte offsets of a tile's four blocks (the host keeps a block
+  // stride under 4 GiB), computed once and used for K in one step and for V
+  // in the next; bit u of `ok` says page u is real (inside the request and
+  // the cache), the others read block 0 and are masked.  (Plain scalars, not
+  // an array: a copy carried across steps must stay in registers.)
+  const uint32_t blk32 = uint32_t(a.block_stride * 2);
+  struct Pages { uint64_t off; int ok; };  // off: this wave's page (page `wave`)
   // Pages [0, pages_here) of the item exist in the request and the index
-  // array; a present page also needs an id in [0, num_blocks).  (Bitwise
-  // tests, no short-circuit branches.)
+  // array; a present page also needs an id in [0, num_blocks).  The four
+  // tests run on lanes 0..3 at once and one ballot collects them.
   const int pages_here = min(npages, last_index - page_off + 1);
   auto resolve = [&](const RawIds& t, int tile) __attribute__((always_inline)) {
-    int32_t id[4];
-    int ok = 0;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int32_t v = __builtin_amdgcn_readfirstlane(t.v[u]);
-      const bool good = (tile * 4 + u < pages_here) & (uint32_t(v) < uint32_t(num_blocks32));
-      ok |= good ? (1 << u) : 0;
-      id[u] = good ? v : 0;
-    }
-    return Pages{id[0], id[1], id[2], id[3], ok};
-  };
-  // Start of a cache block (the host keeps a block under 4 GiB).
-  const uint32_t blk32 = uint32_t(a.block_stride * 2);
-  auto block_at = [&](const char* base, int32_t id) __attribute__((always_inline)) {
-    return base + uint64_t(uint32_t(id)) * blk32;
+    const bool good = (tile * 4 + (lane & 3) < pages_here) & (uint32_t(t.v) < uint32_t(num_blocks32));
+    const int ok = int(__builtin_amdgcn_ballot_w64(good) & 0xF);
+    const int32_t v = good ? t.v : 0;
+    return Pages{uint64_t(uint32_t(__builtin_amdgcn_readlane(v, wave))) * blk32, ok};
   };
   // Direct loads from memory into LDS (global_load_lds_dwordx4 and
   // buffer_load_dwordx4 ... lds, one 16-byte chunk per lane, lane L at LDS
@@ -233,18 +216,17 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
 
   // K goes straight from memory into LDS (global_load_lds_dwordx4): one
   // instruction of a wave fills 1 KB of LDS, lane L's 16 bytes at offset
-  // 16L, so wave w fills keys 16u + 4w .. +3 of page u, and lane L fetches
-  // the chunk that belongs in slot L%16 of key 4w + L/16 of the page.  The
-  // loads are waited for (vmcnt) before the barrier that publishes the tile.
+  // 16L, so load i of wave w fills keys 4i .. 4i+3 of page w (tile rows
+  // 16w + 4i ..), lane L fetching the chunk that belongs in slot L%16 of key
+  // 4i + L/16: one block address per wave and tile.  The loads are waited
+  // for (vmcnt) before the barrier that publishes the tile.
   auto dma_k = [&](KTile& buf, const Pages& p) __attribute__((always_inline)) {
-    const int32_t id[4] = {p.id0, p.id1, p.id2, p.id3};
+    const char* blk = kbase + p.off;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const char* blk = block_at(kbase, id[u]);
+    for (int i = 0; i < 4; ++i)
       asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-                   :: "s"(lds_addr(buf.b + (u * kPage + 4 * wave) * kKRow)), "v"(k_lane_off),
+                   :: "s"(lds_addr(buf.b + (wave * kPage + 4 * i) * kKRow)), "v"(k_lane_off[i]),
                       "s"(blk) : "memory");
-    }
   };
   // V goes into LDS the same way, through a buffer load bounded to the
   // page's valid tokens: lanes past kv_len or in a missing page get zeros
@@ -252,36 +234,28 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   // no such care: a key's score depends on its own K row only, and tiles
   // holding such keys are processed with the per-key tests, which never
   // read its score.
-  auto dma_v_pages = [&](VTile& buf, const Pages& p, const int (&bytes)[4]) __attribute__((always_inline)) {
-    const int32_t id[4] = {p.id0, p.id1, p.id2, p.id3};
+  auto dma_v_page = [&](VTile& buf, const Pages& p, int bytes) __attribute__((always_inline)) {
+    const uint64_t blk = reinterpret_cast<uint64_t>(vbase + p.off);
+    const i32x4_t rsrc = {__builtin_amdgcn_readfirstlane(int(uint32_t(blk))),
+                          __builtin_amdgcn_readfirstlane(int(uint32_t(blk >> 32) & 0xFFFF)),
+                          __builtin_amdgcn_readfirstlane(bytes), kBufferRsrcWord3};
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const uint64_t blk = reinterpret_cast<uint64_t>(block_at(vbase, id[u]));
-      const i32x4_t rsrc = {__builtin_amdgcn_readfirstlane(int(uint32_t(blk))),
-                            __builtin_amdgcn_readfirstlane(int(uint32_t(blk >> 32) & 0xFFFF)),
-                            __builtin_amdgcn_readfirstlane(bytes[u]), kBufferRsrcWord3};
+    for (int i = 0; i < 4; ++i)
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                   :: "s"(lds_addr(buf.b + (u * kPage + 4 * wave) * kKRow)), "v"(v_lane_off),
+                   :: "s"(lds_addr(buf.b + (wave * kPage + 4 * i) * kKRow)), "v"(v_lane_off[i]),
                       "s"(rsrc) : "memory");
-    }
   };
   // Bytes of each page's valid tokens: all 16 on a tile inside the cache
   // (every tile but a request's last), fewer in the page holding kv_len,
   // none in a missing page.
   const int page_bytes = kPage * int(tok_bytes);  // under 2 GiB (host check)
   auto dma_v = [&](VTile& buf, const Pages& p, int tile) __attribute__((always_inline)) {
+    const bool real = (p.ok >> wave) & 1;
     if ((tile + 1) * kKeys <= kv_len) {
-      const int bytes[4] = {(p.ok & 1) ? page_bytes : 0, (p.ok & 2) ? page_bytes : 0,
-                            (p.ok & 4) ? page_bytes : 0, (p.ok & 8) ? page_bytes : 0};
-      dma_v_pages(buf, p, bytes);
+      dma_v_page(buf, p, real ? page_bytes : 0);
     } else {
-      int bytes[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int rem = max(0, min(kPage, kv_len - tile * kKeys - u * kPage));
-        bytes[u] = ((p.ok >> u) & 1) ? rem * int(tok_bytes) : 0;
-      }
-      dma_v_pages(buf, p, bytes);
+      const int rem = max(0, min(kPage, kv_len - tile * kKeys - wave * kPage));
+      dma_v_page(buf, p, real ? rem * int(tok_bytes) : 0);
     }
   };
 
@@ -292,11 +266,11 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   // V tiles start as zeros: should a bounded load leave the LDS rows of
   // out-of-range lanes untouched, they hold zeros or earlier valid rows,
   // never stale bits from before the kernel.  Each wave clears the rows its
-  // own loads fill (rows 16u + 4*wave .. +3 of both buffers) and waits for
-  // that before issuing them.
+  // own loads fill (rows 16*wave .. +15 of both buffers) and waits for that
+  // before issuing them.
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
-    uint8_t* row = vtiles[c >> 2].b + ((c & 3) * kPage + 4 * wave + (lane >> 4)) * kKRow;
+    uint8_t* row = vtiles[c >> 2].b + (wave * kPage + 4 * (c & 3) + (lane >> 4)) * kKRow;
     *reinterpret_cast<uint4*>(row + (lane & 15) * 16) = make_uint4(0, 0, 0, 0);
   }
   __builtin_amdgcn_s_waitcnt(kWaitLgkmcnt0);
@@ -435,7 +409,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   // need the per-key tests.
   f32x16_t s_cur[2];
   int ok_cur = 0;
-  Pages pages_v{0, 0, 0, 0, 0};
+  Pages pages_v{0, 0};
   RawIds raw_k{};
   auto step = [&](int j, auto mc, auto mn, auto has_next) __attribute__((always_inline)) {
     constexpr bool kNext = decltype(has_next)::value;
