@@ -337,6 +337,15 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
       if (visible(rel, ok, q >> 1, e, masked)) mx = fmaxf(mx, s[q >> 1][e]);
     return mx;
   };
+  // The same with the tile's two key blocks held in separate arrays.
+  auto quarter_max2 = [&](const f32x16_t& s0, const f32x16_t& s1, int q, int rel, int ok,
+                          float mx, auto masked) __attribute__((always_inline)) {
+    const f32x16_t& s = (q >> 1) ? s1 : s0;
+#pragma unroll
+    for (int e = 8 * (q & 1); e < 8 * (q & 1) + 8; ++e)
+      if (visible(rel, ok, q >> 1, e, masked)) mx = fmaxf(mx, s[e]);
+    return mx;
+  };
   // Folds a tile's row max (this lane's 32 keys and lane l^32's; the raw
   // scores, as the scale is positive) into the running max.  A row's running
   // max only moves when its max grew by more than kRescaleLog2 (base-2
@@ -393,20 +402,21 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   const int n_full = max(0, min(ntiles, (lim_lo + 1) / kKeys));
 
   // Step j.  On entry: s_cur = raw S^T of tile j, already folded into
-  // m_run; K of tile j+1 staged in ktiles[(j+1)&1] and V of tile j in
-  // vtiles[j&1]; pages_v = pages of tile j+1; raw_k = page ids of tile j+2
-  // (in flight).  A wave issues in order and an MFMA occupies the matrix
-  // pipe for 32 cycles, so the step interleaves, in program order (fenced
-  // with sched_barrier):
+  // m_run; K of tile j+1 in ktiles[(j+1)&1] and V of tile j in vtiles[j&1];
+  // pages_v = pages of tile j+1; raw_k = page ids of tile j+2 (in flight).
+  // The step first issues the direct-to-LDS loads of K of tile j+2 (into the
+  // K buffer tile j used) and V of tile j+1.  A wave issues in order and an
+  // MFMA occupies the matrix pipe for 32 cycles, so the step then
+  // interleaves, in program order (fenced with sched_barrier):
   //   1. the 16 score MFMAs of tile j+1 with the exponentials of tile j,
-  //      one exponent pair per MFMA;
+  //      one exponent pair per MFMA: key block 1's MFMAs first (into s_b1)
+  //      beside block 0's exponentials, then block 0's, straight into
+  //      s_cur[0], which those have finished reading;
   //   2. the 16 MFMAs of O^T += V^T P^T for tile j with the row max of tile
-  //      j+1 and the staging of K of tile j+2 and V of tile j+1 (loaded into
-  //      registers at the start of the step, written into the buffers step
-  //      j-1 read);
+  //      j+1;
   // each with its LDS operand read three MFMAs ahead; then it folds the row
-  // max into m_run and ends on the barrier.  mc / mn: whether tiles j / j+1
-  // need the per-key tests.
+  // max into m_run, moves s_b1 into s_cur[1], waits for its loads and ends
+  // on the barrier.  mc / mn: whether tiles j / j+1 need the per-key tests.
   f32x16_t s_cur[2];
   int ok_cur = 0;
   Pages pages_v{0, 0};
@@ -424,24 +434,28 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
 
     // 1. scores of tile j+1 beside the exponentials of tile j.
     uint32_t pw[2][8];
-    f32x16_t s_nxt[2];
+    f32x16_t s_b1;  // tile j+1's scores, key block 1
     {
       const int rel = rel_of(j);
       float sum0 = 0.f, sum1 = 0.f;
       if constexpr (kNext) {
         const KTile& kb = ktiles[(j + 1) & 1];
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) s_nxt[q][e] = 0.f;
+        // MFMA i computes k-step mi(i) / 2 of key block mi(i) % 2: block 1
+        // for i < 8, block 0 after; each block's k-steps stay in order.
+        auto mi = [](int i) { return i < 8 ? 2 * i + 1 : 2 * (i - 8); };
+        const f32x16_t zero = {};
         bf16x8_t kop[16];
 #pragma unroll
-        for (int i = 0; i < 3; ++i) kop[i] = k_operand(kb, i);
+        for (int i = 0; i < 3; ++i) kop[i] = k_operand(kb, mi(i));
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          if (i + 3 < 16) kop[i + 3] = k_operand(kb, i + 3);
-          s_nxt[i & 1] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[i], qb[i >> 1], s_nxt[i & 1], 0, 0, 0);
+          if (i + 3 < 16) kop[i + 3] = k_operand(kb, mi(i + 3));
+          if (i < 8)
+            s_b1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[i], qb[mi(i) >> 1],
+                                                          i == 0 ? zero : s_b1, 0, 0, 0);
+          else
+            s_cur[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[i], qb[mi(i) >> 1],
+                                                              i == 8 ? zero : s_cur[0], 0, 0, 0);
           exp_pair(s_cur, i, rel, ok_cur, mc, pw, (i & 1) ? sum1 : sum0);
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -452,7 +466,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
       l_half += sum0 + sum1;
     }
 
-    // 2. P_j V_j beside the row max of tile j+1 and the staging.
+    // 2. P_j V_j beside the row max of tile j+1.
     {
       const VTile& vb = vtiles[j & 1];
       const int rel = rel_of(j + 1);
@@ -468,7 +482,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
         const bf16x8_t pb = as_bf16x8(make_uint4(pp[0], pp[1], pp[2], pp[3]));
         o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[i], pb, o[i & 3], 0, 0, 0);
         if constexpr (kNext) {
-          if (i < 4) mx = quarter_max(s_nxt, i, rel, pages_v.ok, mx, mn);
+          if (i < 4) mx = quarter_max2(s_cur[0], s_b1, i, rel, pages_v.ok, mx, mn);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -477,8 +491,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
     wait_dma();
     __syncthreads();
     if constexpr (kNext) {
-#pragma unroll
-      for (int q = 0; q < 2; ++q) s_cur[q] = s_nxt[q];
+      s_cur[1] = s_b1;
       ok_cur = pages_v.ok;
       pages_v = pages_k;
     }
