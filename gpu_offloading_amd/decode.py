@@ -7,8 +7,8 @@
 csrc/decode.hip through libkvc.so.
 
 ``plan`` is host work (plus one small H2D copy), like FlashInfer's: it reads
-the host indptr, cuts the batch's pages into equal segments (the balanced
-split-KV schedule of kvc_decode_plan) and stages the schedule, indptr, indices
+the host indptr, cuts the batch's pages into segments of equal cost (the
+balanced split-KV schedule of kvc_decode_plan) and stages the schedule, indptr, indices
 and last_page_len on the device.  ``run`` launches the streaming kernel and,
 when a request spans more than one segment, the merge kernel.  ``plan`` must be
 called again whenever the sequence lengths change (the engine re-plans every
