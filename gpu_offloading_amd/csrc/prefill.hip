@@ -482,7 +482,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
         const bf16x8_t pb = as_bf16x8(make_uint4(pp[0], pp[1], pp[2], pp[3]));
         o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[i], pb, o[i & 3], 0, 0, 0);
         if constexpr (kNext) {
-          if (i < 4) mx = quarter_max2(s_cur[0], s_b1, i, rel, pages_v.ok, mx, mn);
+          // key block 1 first: block 0's last MFMA has just been issued
+          if (i < 4) mx = quarter_max2(s_cur[0], s_b1, i ^ 2, rel, pages_v.ok, mx, mn);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
