@@ -1103,17 +1103,27 @@ std::vector<int64_t> cut_segments(const int32_t* indptr, int batch, int64_t tota
   std::vector<int64_t> starts;
   for (int b = 1; b < batch; ++b)
     if (indptr[b + 1] > indptr[b] && indptr[b] > 0) starts.push_back(indptr[b]);
+  // F(x) = cost of pages [0, x): cut s goes where F is nearest to s/segs of
+  // the total, so a cut can land exactly on a request's first page (which
+  // then costs no switch: F counts it in the segment it starts).
   const __int128 T = __int128(kPageCost) * total + __int128(kSwitchCost) * int64_t(starts.size());
+  auto F = [&](int64_t x, int64_t below) { return __int128(kPageCost) * x + __int128(kSwitchCost) * below; };
   int64_t x = 0, below = 0;  // below = starts < x
   size_t next = 0;
   bool ok = true;
   for (int64_t s = 1; s < segs; ++s) {
     const __int128 target = __int128(s) * T / segs;
-    while (x < total && __int128(kPageCost) * x + __int128(kSwitchCost) * below < target) {
+    while (x < total && F(x, below) < target) {
       ++x;
       while (next < starts.size() && starts[next] < x) ++below, ++next;
     }
-    cut[size_t(s)] = std::min(std::max(x, cut[size_t(s) - 1] + 1), total - (segs - s));
+    // x is the first page with F(x) >= target; x - 1 may be nearer
+    int64_t pick = x;
+    if (x > 0) {
+      const int64_t below_prev = below - ((next > 0 && starts[next - 1] == x - 1) ? 1 : 0);
+      if (target - F(x - 1, below_prev) < F(x, below) - target) pick = x - 1;
+    }
+    cut[size_t(s)] = std::min(std::max(pick, cut[size_t(s) - 1] + 1), total - (segs - s));
     ok = ok && cut[size_t(s)] - cut[size_t(s) - 1] <= kMaxSegPages;
   }
   ok = ok && total - cut[size_t(segs) - 1] <= kMaxSegPages;

@@ -276,6 +276,31 @@ def test_noalloc_run_refuses_partials_beyond_its_array_on_the_host(lib):
                                             None, None) == 0
 
 
+@pytest.mark.parametrize("lens, hint, starts", [
+    # four 10-page requests, four segments: cut on the request boundaries
+    # (no request split, so no partials at all)
+    ([160] * 4, 4, [0, 10, 20, 30]),
+    # pages 6, 30, 4: cost 8 x 40 + 9 x 2 switches = 338; the cut at page 20
+    # gives 8 x 20 + 9 (the switch at page 6) = 169 on each side
+    ([96, 480, 64], 2, [0, 20]),
+    # pages 2, 2, 2, 2, 32: cost 320 + 4 x 9 = 356, half 178; F(17) = 136 +
+    # 36 = 172 and F(18) = 144 + 36 = 180, so the cut is page 18, two pages
+    # before the equal-page cut: segment 0 (18 pages, 4 switches) costs 180,
+    # segment 1 (22 pages) 176
+    ([32, 32, 32, 32, 512], 2, [0, 18]),
+])
+def test_decode_plan_cuts_balance_pages_and_switches(lib, lens, hint, starts):
+    """Segment cuts, worked by hand: a page costs 8, a switch to another
+    request inside a segment 9 more; each cut goes where the cost of the pages
+    before it is nearest to its share of the total."""
+    indptr, sched, img, lpl = _plan(lib, lens, hint=hint)
+    _check_plan_image(indptr, sched, img, lpl)
+    segs = img[:4 * sched.num_segments].reshape(-1, 4)
+    assert segs[:, 2].tolist() == starts
+    if starts == [0, 10, 20, 30]:
+        assert sched.max_partitions == 1 and sched.workspace_bytes == 0
+
+
 def test_decode_plan_random_batches(lib):
     rng = np.random.default_rng(0)
     for trial in range(30):
