@@ -629,11 +629,12 @@ def run_small_batch(torch, seed, layers=20, steps=50):
     src/MoE/pipeline_parallelism.md:144) and 0.258 ms of step setup
     (pipeline_parallelism.md:81).  Reported: the decode launch alone (event
     time per launch over back-to-back launches), one step (setup + 20 fused
-    append + decode launches, event time), and the host time of the step
+    append + decode launches, event time), the same step with its 20
+    launches replayed from a HIP graph, and the host time of the step
     setup."""
     from gpu_offloading_amd.kv_cache import PagedKVCache
 
-    cache = PagedKVCache(layers, 8, 128, max_seqs=1, max_seq_len=128 + steps + 64,
+    cache = PagedKVCache(layers, 8, 128, max_seqs=1, max_seq_len=128 + 2 * steps + 64,
                          num_qo_heads=32, kv_page_budget=64, device="cuda",
                          workspace_bytes=1 << 22, staging_bytes=1 << 20)
     g = torch.Generator(device="cuda")
@@ -667,13 +668,47 @@ def run_small_batch(torch, seed, layers=20, steps=50):
     torch.cuda.synchronize()
     step_ms = e0.elapsed_time(e1) / steps
     t_dec = _timed_rounds(torch, lambda: cache.decode(0, q, out=out), 100)
+
+    # The same steps with the 20 fused launches captured once in a HIP graph
+    # and replayed after each step's setup: the kernels read the step's plan,
+    # lengths and page ids from the cache's step buffer (decode_graph_key
+    # says when a new capture is needed).
+    graph, key, captures = None, None, [0]
+
+    def graph_step():
+        nonlocal graph, key
+        cache.ensure_pages(0, (int(cache._seq_lens_cpu[0]) + 1 + 15) // 16)
+        cache.prepare_decode_step([0])
+        if cache.decode_graph_key() != key:
+            captures[0] += 1
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for layer in range(layers):
+                    cache.append_and_decode(layer, nk, nv, q, out=out)
+            key = cache.decode_graph_key()
+        graph.replay()
+
+    for _ in range(5):
+        graph_step()
+    torch.cuda.synchronize()
+    warm_captures = captures[0]
+    e0.record()
+    for _ in range(steps):
+        graph_step()
+    e1.record()
+    torch.cuda.synchronize()
+    graph_ms = e0.elapsed_time(e1) / steps
+    log(f"bs1: graph captures {warm_captures} in warm-up, {captures[0] - warm_captures} timed")
     res = {"decode_launch_us": t_dec * 1e6, "step_ms_20_layers": step_ms,
            "per_layer_us": step_ms * 1e3 / layers,
+           "step_ms_20_layers_graph": graph_ms,
+           "per_layer_us_graph": graph_ms * 1e3 / layers,
            "step_setup_host_ms": 1e3 * sorted(setups)[len(setups) // 2],
            "shape": "B=1, ctx 128 (+1 per step), Hkv 8, Hq 32, D 128, 20 layers"}
     log(f"bs1: decode launch {res['decode_launch_us']:.1f} us, step {step_ms:.3f} ms for "
         f"{layers} layers ({res['per_layer_us']:.1f} us/layer), setup "
-        f"{res['step_setup_host_ms']:.3f} ms host")
+        f"{res['step_setup_host_ms']:.3f} ms host; graph-replayed step {graph_ms:.3f} ms "
+        f"({res['per_layer_us_graph']:.1f} us/layer)")
     del cache
     torch.cuda.empty_cache()
     return res

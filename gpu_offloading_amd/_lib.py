@@ -139,6 +139,7 @@ SIGNATURES = {
         c_int32, c_int32, c_int32, c_int32, _P, _I32P, _P]),
     "kvc_copy_page_indices": (c_int, [
         _I32P, c_int64, c_int32, _I32P, _I32P, c_int32, c_int32, _I32P, c_int64, _P]),
+    "kvc_stage_from_host": (c_int, [_I32P, _I32P, c_int64, c_int64, c_int64, _P]),
 }
 
 _lock = threading.Lock()

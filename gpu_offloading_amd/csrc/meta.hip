@@ -11,6 +11,15 @@
 // index_select (moe_engine.py:1937-1946): the first indptr[r+1]-indptr[r]
 // entries of block-table row seq_ids[r] are flattened into indices[indptr[r]:]
 // (clamped to the buffer's capacity).
+//
+// kvc_stage_from_host stands for the engine's pinned-buffer .copy_(...,
+// non_blocking=True) uploads of the step metadata (moe_engine.py:3493-3494,
+// 3506-3507): one kernel on the caller's stream reads the step's pinned int32
+// image over the host link and writes it to device memory.  A hipMemcpyAsync
+// of pinned memory runs on a copy engine: the compute queue then waits on it,
+// and when that queue is still busy with the previous step (a replayed
+// graph) the host thread issuing the copy was measured blocked for hundreds
+// of microseconds.
 #include "kvc_common.h"
 
 #include <algorithm>
@@ -81,10 +90,63 @@ __global__ __launch_bounds__(256) void copy_page_indices_kernel(
   for (int j = threadIdx.x; j < n; j += 256) indices[beg + j] = src[j];
 }
 
+// Four int32 per thread: ranges [0, head) and [tail_begin, tail_end) of the
+// image, tail_begin a multiple of 4, both buffers 16-byte aligned.  The host
+// loads are system-scope, so they read memory, not a cached older image.
+__global__ __launch_bounds__(256) void stage_kernel(const int32_t* __restrict__ host,
+                                                    int32_t* __restrict__ dev, int64_t head,
+                                                    int64_t tail_begin, int64_t tail_end) {
+  int64_t q = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t head_quads = (head + 3) >> 2;
+  int64_t beg, end;
+  if (q < head_quads) {
+    beg = q << 2;
+    end = min(beg + 4, head);
+  } else {
+    beg = tail_begin + ((q - head_quads) << 2);
+    if (beg >= tail_end) return;
+    end = min(beg + 4, tail_end);
+  }
+  if (end - beg == 4) {
+    const uint64_t* s = reinterpret_cast<const uint64_t*>(host + beg);
+    const uint64_t lo = __hip_atomic_load(s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const uint64_t hi = __hip_atomic_load(s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    *reinterpret_cast<uint4*>(dev + beg) =
+        make_uint4(uint32_t(lo), uint32_t(lo >> 32), uint32_t(hi), uint32_t(hi >> 32));
+  } else {
+    for (int64_t i = beg; i < end; ++i)
+      dev[i] = __hip_atomic_load(host + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
 }  // namespace
 }  // namespace kvc
 
 using namespace kvc;
+
+extern "C" int kvc_stage_from_host(const int32_t* host, int32_t* dev, int64_t head,
+                                   int64_t tail_begin, int64_t tail_end, void* stream) {
+  KVC_REQUIRE(head >= 0 && tail_begin >= head && tail_end >= tail_begin,
+              KVC_ERR_INVALID_ARG, "need 0 <= head <= tail_begin <= tail_end");
+  KVC_REQUIRE((tail_begin & 3) == 0, KVC_ERR_INVALID_ARG, "tail_begin must be a multiple of 4");
+  const int64_t quads = ((head + 3) >> 2) + ((tail_end - tail_begin + 3) >> 2);
+  if (quads == 0) return ok();
+  KVC_REQUIRE(host && dev, KVC_ERR_INVALID_ARG, "null pointer");
+  KVC_REQUIRE((reinterpret_cast<uintptr_t>(host) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(dev) & 15) == 0,
+              KVC_ERR_INVALID_ARG, "host and dev must be 16-byte aligned");
+  // The image must be pinned host memory the device can read; the kernel
+  // uses the device's address of it.
+  hipPointerAttribute_t attr{};
+  const hipError_t e = hipPointerGetAttributes(&attr, host);
+  if (e != hipSuccess) (void)hipGetLastError();  // not sticky: clear it for later checks
+  KVC_REQUIRE(e == hipSuccess && attr.type == hipMemoryTypeHost && attr.devicePointer,
+              KVC_ERR_INVALID_ARG, "host image is not pinned host memory (hipHostMalloc)");
+  stage_kernel<<<dim3(unsigned(cdiv(quads, 256))), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const int32_t*>(attr.devicePointer), dev, head, tail_begin, tail_end);
+  KVC_LAUNCH_CHECK();
+  return ok();
+}
 
 extern "C" int kvc_compute_slot_mapping(
     const int32_t* block_table, int64_t block_table_row_stride, int32_t block_table_rows,

@@ -125,6 +125,8 @@ class PagedKVCache:
         self._bt_pending: dict[int, int] = {}
         # slots of the step set up by prepare_decode_step (append_and_decode)
         self._step_slots: Optional[torch.Tensor] = None
+        # device copy of a decode step's metadata image (reused every step)
+        self._step_dev: Optional[torch.Tensor] = None
         self.seq_lens = torch.zeros(max_seqs, dtype=torch.int32, device=self.device)
         self._seq_lens_cpu = torch.zeros(max_seqs, dtype=torch.int32)
         self._pool = PagePool(self.total_pages, max_seqs, self.max_pages_per_seq,
@@ -135,6 +137,13 @@ class PagedKVCache:
         self._decode_wrapper: Optional[BatchDecodeWithPagedKVCacheWrapper] = None
         if self.device.type == "cuda":
             self._init_step_buffers()
+
+        # Pinned images of the step metadata, reused round-robin: a fresh
+        # pinned tensor per step costs a host allocation (and a wait) whenever
+        # the host runs ahead of the GPU, as it does when the layers are
+        # replayed from a graph.  Each slot: [buffer, event of its last copy].
+        self._meta_ring: list[list] = [[None, None] for _ in range(4)]
+        self._meta_next = 0
 
         self._staging_bytes = staging_bytes
         self._staging: Optional[torch.Tensor] = None
@@ -480,24 +489,28 @@ class PagedKVCache:
                 raise RuntimeError(f"sequences {short} have no page for the new token "
                                    "(ensure_pages first)")
 
-        # One pinned int32 image of the step's metadata, one H2D copy:
-        #   ids[b] | qsl[b+1] | lens_before[ms] | lens_after[ms] | kv_indptr[b+1]
-        #   | last_page_len[b] | block-table positions (int64) | page ids
-        #   | decode schedule (16-byte aligned)
+        # One pinned int32 image of the step's metadata, one upload into the
+        # cache's step buffer (the same device memory every step, so a decode
+        # launch captured in a graph reads the new plan when replayed):
+        #   decode schedule (cap, 16-byte aligned) | ids[b] | qsl[b+1]
+        #   | lens_before[ms] | lens_after[ms] | kv_indptr[b+1] | last_page_len[b]
+        #   | block-table positions (int64) | page ids
         pend = self._peek_bt_pending()
         u = 0 if pend is None else len(pend[0])
         w = self._decode_wrapper
-        o_ids, o_qsl = 0, b
-        o_lb = o_qsl + b + 1
-        o_la = o_lb + ms
-        o_ip = o_la + ms
-        o_lpl = o_ip + b + 1
-        o_pos = (o_lpl + b + 1) // 2 * 2
-        o_val = o_pos + 2 * u
-        o_plan = (o_val + u + 3) // 4 * 4
         cap = w._plan_capacity(b)
         while True:
-            hs = torch.empty(o_plan + cap, dtype=torch.int32, pin_memory=True)
+            o_plan = 0
+            o_ids = cap
+            o_qsl = o_ids + b
+            o_lb = o_qsl + b + 1
+            o_la = o_lb + ms
+            o_ip = o_la + ms
+            o_lpl = o_ip + b + 1
+            o_pos = (o_lpl + b + 1) // 2 * 2
+            o_val = o_pos + 2 * u
+            n = o_val + u
+            hs = self._host_image(n)
             h = hs.numpy()
             h[o_ids:o_qsl] = ids
             h[o_qsl:o_lb] = np.arange(b + 1, dtype=np.int32)
@@ -514,13 +527,22 @@ class PagedKVCache:
                 h[o_val:o_val + u] = pend[1]
             sched = w._schedule_into(h[o_ip:o_ip + b + 1], h[o_lpl:o_lpl + b], b,
                                      self.num_heads, self.num_kv_heads, self.head_dim, ps,
-                                     hs[o_plan:])
+                                     hs[o_plan:o_plan + cap])
             if sched.plan_ints <= cap:
                 break
             cap = (sched.plan_ints + 3) // 4 * 4
         total = int(h[o_ip + b])
 
-        dm = hs.to(self.device, non_blocking=True)
+        if self._step_dev is None or self._step_dev.numel() < n:
+            # grows rarely (more requests or block-table writes than before);
+            # a graph captured before must then be captured again
+            self._step_dev = torch.empty(2 * max(n, 0 if self._step_dev is None
+                                                 else self._step_dev.numel()),
+                                         dtype=torch.int32, device=self.device)
+        dm = self._step_dev[:n]
+        # The plan's unused capacity is not sent.
+        ops.stage_from_host(hs, dm, int(sched.plan_ints), cap, n)
+        self._host_image_sent()
         if u:
             self._bt.view(-1).scatter_(0, dm[o_pos:o_val].view(torch.int64), dm[o_val:o_val + u])
             self._bt_pending.clear()
@@ -531,12 +553,33 @@ class PagedKVCache:
         self.seq_lens.copy_(dm[o_la:o_ip])
         indptr_d = dm[o_ip:o_lpl]
         ops.copy_page_indices(self._bt, indptr_d, self._plan_indices_gpu, seq_ids=ids_d)
+        # The whole page-index buffer goes to the decode (its pages are bounded
+        # by the plan), so the launch does not change with the page count.
         w._install(sched, dm[o_plan:o_plan + cap], indptr_d, dm[o_lpl:o_lpl + b],
-                   self._plan_indices_gpu[:total], self.num_heads, self.num_kv_heads,
+                   self._plan_indices_gpu, self.num_heads, self.num_kv_heads,
                    self.head_dim, ps)
         lens_all[ids] += 1
         self._step_slots = slots[:b]
         return slots
+
+    def decode_graph_key(self) -> tuple:
+        """What a decode launch of the current step bakes in besides its
+        tensors: the device address of the step's plan and the launch shape of
+        its schedule.  A graph that captured ``append_and_decode`` /
+        ``decode`` calls after ``prepare_decode_step`` can be replayed after
+        later ``prepare_decode_step`` calls while this key stays the same (the
+        kernels read the new plan, lengths and page ids from the same
+        buffers); when it changes, capture again."""
+        w = self._decode_wrapper
+        s = w.schedule
+        if s is None or self._step_dev is None or self._step_slots is None:
+            return ()
+        # Without the fused append, append_and_decode's separate append reads
+        # the step's slot tensor, a new allocation every step.
+        slots = 0 if w.fused_append_supported else self._step_slots.data_ptr()
+        return (self._step_dev.data_ptr(), slots, s.batch, s.small_batch, s.num_segments,
+                s.num_head_groups, s.heads_per_group, s.max_partitions, s.num_empty > 0,
+                s.pieces_offset, s.nparts_offset, s.append_pieces)
 
     def prepare_step(self, decode_seq_ids: Sequence[int] = (),
                      prefill_seq_ids: Sequence[int] = (), prefill_lens: Sequence[int] = (),
@@ -627,7 +670,7 @@ class PagedKVCache:
         dcap = dw._plan_capacity(D) if D else 0
         while True:
             o_pplan = o_dplan + dcap
-            hs = torch.empty(o_pplan + pcap, dtype=torch.int32, pin_memory=True)
+            hs = self._host_image(o_pplan + pcap)
             h = hs.numpy()
             h[:R] = ids
             h[o_qsl] = 0
@@ -663,7 +706,11 @@ class PagedKVCache:
         self._check_page_counts(np.concatenate([(d_after + ps - 1) // ps,
                                                 (c_after + ps - 1) // ps]))
 
-        dm = hs.to(self.device, non_blocking=True)           # the step's one H2D copy
+        # The step's one upload; the plans' unused capacity is not sent.
+        dm = torch.empty(hs.numel(), dtype=torch.int32, device=self.device)
+        ops.stage_from_host(hs, dm, o_dplan + (int(dsched.plan_ints) if D else 0),
+                            o_pplan, o_pplan + (int(psched.plan_ints) if C else 0))
+        self._host_image_sent()
         if u:
             self._bt.view(-1).scatter_(0, dm[o_pos:o_val].view(torch.int64), dm[o_val:o_val + u])
             self._bt_pending.clear()
@@ -765,6 +812,27 @@ class PagedKVCache:
         if self._copy_stream is None:
             self._copy_stream = torch.cuda.Stream(device=self.device)
         return self._copy_stream
+
+    def _host_image(self, n: int) -> torch.Tensor:
+        """A pinned int32 image of ``n`` entries for the step's metadata: the
+        ring's next slot, once the copy that last read it has run (the host
+        stays at most four steps ahead of the GPU)."""
+        slot = self._meta_ring[self._meta_next]
+        if slot[1] is not None:
+            slot[1].synchronize()
+        if slot[0] is None or slot[0].numel() < n:
+            slot[0] = torch.empty(max(n, 2 * (0 if slot[0] is None else slot[0].numel())),
+                                  dtype=torch.int32, pin_memory=True)
+        return slot[0][:n]
+
+    def _host_image_sent(self) -> None:
+        """Mark the slot ``_host_image`` returned as read by the copy just
+        issued on the current stream, and move to the next slot."""
+        slot = self._meta_ring[self._meta_next]
+        if slot[1] is None:
+            slot[1] = torch.cuda.Event()
+        slot[1].record()
+        self._meta_next = (self._meta_next + 1) % len(self._meta_ring)
 
     def _staging_buf(self) -> torch.Tensor:
         if self._staging is None:

@@ -10,6 +10,7 @@ Reference call sites (aojsd/GPU_Offloading):
   merge_attention_states    src/dense/offload_kv_attn.py:24-39
   compute_slot_mapping      src/MoE/moe_engine.py:3514-3541 (eager :1308-1316)
   copy_page_indices         src/MoE/moe_engine.py:1937-1946
+  stage_from_host           src/MoE/moe_engine.py:3493-3494, 3506-3507
   gather_kv / *_blocks / swap_*   new API (the engine has no gather or swap;
                             precedents moe_engine.py:4163-4183 and
                             src/dense/include/paged_offload_transformer.py:111-134, 394-418)
@@ -28,6 +29,7 @@ __all__ = [
     "merge_attention_states",
     "compute_slot_mapping",
     "copy_page_indices",
+    "stage_from_host",
     "gather_blocks",
     "scatter_blocks",
     "swap_out_blocks",
@@ -281,6 +283,34 @@ def copy_page_indices(block_table: torch.Tensor, indptr: torch.Tensor,
               block_table.shape[1], indices.data_ptr(), indices.numel(),
               _stream_handle(dev, stream))
     return indices
+
+
+def stage_from_host(host: torch.Tensor, dev: torch.Tensor, head: int,
+                    tail_begin: int = 0, tail_end: int = 0, *,
+                    stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """``dev[i] = host[i]`` for i in ``[0, head)`` and ``[tail_begin,
+    tail_end)``: the engine's pinned-buffer uploads of step metadata
+    (moe_engine.py:3493-3494, 3506-3507) as one kernel on the compute stream,
+    which reads the pinned int32 ``host`` when it runs (keep it unchanged
+    until then: record an event after the call)."""
+    dev_ = _check_cuda(dev)
+    if host.is_cuda or not host.is_pinned():
+        _fail("host must be a pinned CPU tensor")
+    if host.dtype != torch.int32 or dev.dtype != torch.int32:
+        _fail("host and dev must be int32")
+    if not (host.is_contiguous() and dev.is_contiguous()):
+        _fail("host and dev must be contiguous")
+    n = min(host.numel(), dev.numel())
+    if tail_end == 0:
+        tail_begin = tail_end = (head + 3) // 4 * 4      # no tail range
+        if not 0 <= head <= n:
+            _fail(f"range [0, {head}) does not fit host[{host.numel()}] / dev[{dev.numel()}]")
+    elif not (0 <= head <= tail_begin <= tail_end <= n):
+        _fail(f"ranges [0, {head}) and [{tail_begin}, {tail_end}) do not fit "
+              f"host[{host.numel()}] / dev[{dev.numel()}]")
+    _lib.call("kvc_stage_from_host", host.data_ptr(), dev.data_ptr(), head, tail_begin,
+              tail_end, _stream_handle(dev_, stream))
+    return dev
 
 
 # --------------------------------------------------------------------------

@@ -427,6 +427,20 @@ int kvc_copy_page_indices(const int32_t* block_table,
                           int32_t num_reqs, int32_t max_pages_per_req,
                           int32_t* indices, int64_t indices_capacity, void* stream);
 
+/* kvc_stage_from_host replaces the pinned-buffer .copy_(..., non_blocking=True)
+ * uploads of the step metadata at src/MoE/moe_engine.py:3493-3494, 3506-3507
+ * with one kernel on `stream`:
+ *   dev[i] = host[i]  for i in [0, head) and [tail_begin, tail_end)   (int32)
+ * read from the pinned image when the kernel runs, so `host` must stay
+ * unchanged until then (wait for an event recorded after this call).  `host`
+ * must be pinned host memory (hipHostMalloc, torch pin_memory) and both
+ * buffers 16-byte aligned; tail_begin is a multiple of 4 and
+ * 0 <= head <= tail_begin <= tail_end.  The upload runs on the compute queue:
+ * a hipMemcpyAsync of pinned memory goes to a copy engine, which the compute
+ * queue then waits for. */
+int kvc_stage_from_host(const int32_t* host, int32_t* dev, int64_t head,
+                        int64_t tail_begin, int64_t tail_end, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

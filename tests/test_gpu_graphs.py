@@ -72,3 +72,71 @@ def test_graph_mode_wrappers_are_refused(gpu):
         BatchDecodeWithPagedKVCacheWrapper(ws, "NHD", use_cuda_graph=True)
     with pytest.raises(RuntimeError, match="use_cuda_graph"):
         BatchPrefillWithPagedKVCacheWrapper(ws, "NHD", use_cuda_graph=True)
+
+
+def test_decode_step_graph_replays_across_planned_steps(gpu):
+    """A whole decode step of a PagedKVCache (fused append + decode on every
+    layer) captured once and replayed after each later prepare_decode_step:
+    the kernels read each step's plan, lengths and page ids from the cache's
+    step buffer, so every replay equals an eager twin cache bit for bit
+    (outputs and cache contents), across page allocations, while
+    decode_graph_key() holds; when it changes (here a request outgrows the
+    small-batch schedule) the step is captured again."""
+    from gpu_offloading_amd.kv_cache import PagedKVCache
+
+    layers, hkv, hq = 3, 8, 32
+    seqs, lens = [0, 1, 2], [100, 46, 250]
+
+    def make():
+        c = PagedKVCache(layers, hkv, 128, max_seqs=4, max_seq_len=512, num_qo_heads=hq,
+                         kv_page_budget=96, device=gpu, workspace_bytes=1 << 22,
+                         staging_bytes=1 << 20)
+        c.fill_kv_random(1.0, generator=torch.Generator(device=gpu).manual_seed(7))
+        for s, ln in zip(seqs, lens):
+            c.ensure_pages(s, (ln + 15) // 16)
+        c.advance(seqs, lens)
+        return c
+
+    eager, graphed = make(), make()
+    g = torch.Generator(device=gpu).manual_seed(8)
+    bf = torch.bfloat16
+    q = [torch.zeros(3, hq, 128, dtype=bf, device=gpu) for _ in range(layers)]
+    k = [torch.zeros(3, hkv, 128, dtype=bf, device=gpu) for _ in range(layers)]
+    v = [torch.zeros(3, hkv, 128, dtype=bf, device=gpu) for _ in range(layers)]
+    out_e = [torch.empty_like(t) for t in q]
+    out_g = [torch.empty_like(t) for t in q]
+    graph, key, captures, reuses, kinds = None, None, 0, 0, set()
+    for step in range(12):
+        for t in q + k + v:   # eager work between replays: new inputs in place
+            t.copy_(torch.randn(t.shape, generator=g, device=gpu).to(bf))
+        for c in (eager, graphed):
+            for s in seqs:
+                c.ensure_pages(s, (int(c._seq_lens_cpu[s]) + 1 + 15) // 16)
+            c.prepare_decode_step(seqs)
+        for layer in range(layers):
+            eager.append_and_decode(layer, k[layer], v[layer], q[layer], out=out_e[layer])
+        kinds.add(graphed._decode_wrapper.schedule.small_batch)
+        if graphed.decode_graph_key() != key:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for layer in range(layers):
+                    graphed.append_and_decode(layer, k[layer], v[layer], q[layer],
+                                              out=out_g[layer])
+            key = graphed.decode_graph_key()
+            captures += 1
+        else:
+            reuses += 1
+        graph.replay()
+        torch.cuda.synchronize()
+        for layer in range(layers):
+            assert torch.equal(out_g[layer], out_e[layer]), (step, layer)
+            assert torch.equal(graphed.k_cache[layer], eager.k_cache[layer]), (step, layer)
+            assert torch.equal(graphed.v_cache[layer], eager.v_cache[layer]), (step, layer)
+    # Both schedules ran: small-batch for steps 0-5, then request 2 passed 16
+    # pages (257 tokens) at step 6.  Each was captured once and replayed for
+    # the other steps, the first across request 1's new page at step 2 (49
+    # tokens).
+    assert kinds == {0, 1}
+    assert captures == 2 and reuses == 10
+    assert [int(x) for x in graphed._seq_lens_cpu[:3]] == [112, 58, 262]
+    assert graphed.seq_pages(1) == 4

@@ -180,3 +180,61 @@ def test_step_setup_rejects_bad_requests(gpu):
     with pytest.raises(RuntimeError, match="max_seq_len"):
         cache.prepare_decode_step([0])
     assert [int(x) for x in cache._seq_lens_cpu] == [32, 0, 0]
+
+
+@pytest.mark.parametrize("head,tail", [(0, (0, 0)), (5, (8, 8)), (37, (40, 101)), (4096, (4096, 6003)),
+                                       (0, (12, 13))])
+def test_stage_from_host_copies_exactly_the_two_ranges(gpu, head, tail):
+    from gpu_offloading_amd import ops
+
+    n = 6016
+    rng = np.random.default_rng(head + tail[1])
+    host = torch.from_numpy(rng.integers(-2**31, 2**31, n, dtype=np.int64).astype(np.int32)).pin_memory()
+    dev = torch.full((n,), -7, dtype=torch.int32, device=gpu)
+    if tail == (0, 0):
+        ops.stage_from_host(host, dev, head)
+    else:
+        ops.stage_from_host(host, dev, head, *tail)
+    want = np.full(n, -7, np.int32)
+    h = host.numpy()
+    want[:head] = h[:head]
+    want[tail[0]:tail[1]] = h[tail[0]:tail[1]]
+    np.testing.assert_array_equal(dev.cpu().numpy(), want)
+
+
+def test_stage_from_host_reads_the_image_when_it_runs(gpu):
+    """A slot rewritten after the event of its upload has fired is read anew:
+    the upload does not see a cached older image."""
+    from gpu_offloading_amd import ops
+
+    host = torch.zeros(4096, dtype=torch.int32).pin_memory()
+    dev = torch.empty(4096, dtype=torch.int32, device=gpu)
+    for i in range(5):
+        host.fill_(i * 1000 + 1)
+        host[::7] = -i
+        ops.stage_from_host(host, dev, 4096)
+        ev = torch.cuda.Event()
+        ev.record()
+        ev.synchronize()
+        np.testing.assert_array_equal(dev.cpu().numpy(), host.numpy())
+
+
+def test_stage_from_host_rejects_bad_buffers(gpu):
+    from gpu_offloading_amd import _lib, ops
+
+    dev = torch.zeros(64, dtype=torch.int32, device=gpu)
+    with pytest.raises(RuntimeError, match="pinned"):
+        ops.stage_from_host(torch.zeros(64, dtype=torch.int32), dev, 8)
+    pinned = torch.zeros(64, dtype=torch.int32).pin_memory()
+    with pytest.raises(RuntimeError, match="do not fit"):
+        ops.stage_from_host(pinned, dev, 8, 16, 65)
+    # The C entry checks the memory itself: pageable memory is refused, and
+    # the failed query leaves no error behind for the next launch.
+    pageable = torch.zeros(64, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="not pinned"):
+        _lib.call("kvc_stage_from_host", pageable.data_ptr(), dev.data_ptr(), 8, 8, 8, None)
+    with pytest.raises(RuntimeError, match="multiple of 4"):
+        _lib.call("kvc_stage_from_host", pinned.data_ptr(), dev.data_ptr(), 8, 10, 12, None)
+    pinned[:] = torch.arange(64, dtype=torch.int32)
+    ops.stage_from_host(pinned, dev, 64)
+    np.testing.assert_array_equal(dev.cpu().numpy(), np.arange(64))
