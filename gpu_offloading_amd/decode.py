@@ -72,7 +72,9 @@ class BatchDecodeWithPagedKVCacheWrapper:
         self._num_indices = 0
         self._sm_scale = None
         self._plan_args = None
-        self._kv_checked = None   # (k ref, v ref, (ps, hkv, d), k geometry, v geometry)
+        # (id(k), id(v)) -> (k ref, v ref, (ps, hkv, d), k geometry, v geometry)
+        # for the cache tensors already checked (one pair per layer).
+        self._kv_checked: dict = {}
 
     # ------------------------------------------------------------------ plan
     def plan(self, indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
@@ -318,7 +320,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
         # The per-layer cache views are the same tensor objects call after
         # call: once checked against this (page_size, heads, dim) they are
         # only compared by identity, shape and strides.
-        seen = self._kv_checked
+        seen = self._kv_checked.get((id(k_cache), id(v_cache)))
         if (seen is not None and seen[0]() is k_cache and seen[1]() is v_cache
                 and seen[2] == (ps, hkv, d) and seen[3] == (k_cache.shape, k_cache.stride())
                 and seen[4] == (v_cache.shape, v_cache.stride())):
@@ -334,8 +336,11 @@ class BatchDecodeWithPagedKVCacheWrapper:
                 _fail(f"{name} on {c.device}, workspace on {self._device}")
         if k_cache.stride() != v_cache.stride() or k_cache.shape[0] != v_cache.shape[0]:
             _fail("k_cache and v_cache must share shape and strides")
-        self._kv_checked = (weakref.ref(k_cache), weakref.ref(v_cache), (ps, hkv, d),
-                            (k_cache.shape, k_cache.stride()), (v_cache.shape, v_cache.stride()))
+        if len(self._kv_checked) >= 1024:
+            self._kv_checked.clear()
+        self._kv_checked[(id(k_cache), id(v_cache))] = (
+            weakref.ref(k_cache), weakref.ref(v_cache), (ps, hkv, d),
+            (k_cache.shape, k_cache.stride()), (v_cache.shape, v_cache.stride()))
         return k_cache, v_cache, *self._out_args(q, out, lse, return_lse)
 
     def _out_args(self, q, out, lse, return_lse):
