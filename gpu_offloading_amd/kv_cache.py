@@ -572,12 +572,14 @@ class PagedKVCache:
         buffers); when it changes, capture again."""
         w = self._decode_wrapper
         s = w.schedule
-        if s is None or self._step_dev is None or self._step_slots is None:
-            return ()
+        if (s is None or self._step_dev is None or self._step_slots is None
+                or w._plan_dev.data_ptr() != self._step_dev.data_ptr()):
+            return ()   # no decode step set up (or a mixed step's plan is current)
         # Without the fused append, append_and_decode's separate append reads
         # the step's slot tensor, a new allocation every step.
         slots = 0 if w.fused_append_supported else self._step_slots.data_ptr()
-        return (self._step_dev.data_ptr(), slots, s.batch, s.small_batch, s.num_segments,
+        return (self._step_dev.data_ptr(), w._indices.data_ptr(), w._num_indices, slots,
+                s.batch, s.small_batch, s.num_segments,
                 s.num_head_groups, s.heads_per_group, s.max_partitions, s.num_empty > 0,
                 s.pieces_offset, s.nparts_offset, s.append_pieces)
 

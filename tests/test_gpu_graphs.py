@@ -140,3 +140,32 @@ def test_decode_step_graph_replays_across_planned_steps(gpu):
     assert captures == 2 and reuses == 10
     assert [int(x) for x in graphed._seq_lens_cpu[:3]] == [112, 58, 262]
     assert graphed.seq_pages(1) == 4
+
+
+def test_decode_graph_key_is_empty_when_the_step_buffer_plan_is_not_current(gpu):
+    """decode_graph_key() names the decode step's buffer only while its plan
+    is the one the wrapper runs: after a mixed step (whose plan lives in that
+    step's own upload) it is empty, so no graph captured for a decode step is
+    replayed against another plan; the next decode step restores it."""
+    from gpu_offloading_amd.kv_cache import PagedKVCache
+
+    c = PagedKVCache(1, 8, 128, max_seqs=4, max_seq_len=512, num_qo_heads=32,
+                     kv_page_budget=64, device=gpu, workspace_bytes=1 << 22,
+                     staging_bytes=1 << 20)
+    assert c.decode_graph_key() == ()
+    c.ensure_pages(0, 3)
+    c.ensure_pages(1, 2)
+    c.advance([0, 1], [40, 20])
+    for s, ln in ((0, 41), (1, 21)):
+        c.ensure_pages(s, (ln + 15) // 16)
+    c.prepare_decode_step([0, 1])
+    key = c.decode_graph_key()
+    assert key != ()
+    c.ensure_pages(0, 3)
+    c.ensure_pages(2, 2)
+    c.prepare_step(decode_seq_ids=[0], prefill_seq_ids=[2], prefill_lens=[17])
+    assert c.decode_graph_key() == ()
+    for s in (0, 1):
+        c.ensure_pages(s, (int(c._seq_lens_cpu[s]) + 1 + 15) // 16)
+    c.prepare_decode_step([0, 1])
+    assert c.decode_graph_key() == key
