@@ -116,7 +116,8 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 // key tile is about as long as the tile's 32 MFMAs, so each wave runs them
 // side by side: step j computes the softmax of tile j while the MFMAs of the
 // scores of tile j+1 run, then P_j V_j while the next tiles are staged.  The
-// softmax is kept lean: per-key tests only on boundary tiles, the scale folded
+// softmax is kept lean: per-key tests only on boundary tiles, once per score
+// (hidden scores set to -inf while the row max is taken), the scale folded
 // into one FMA per score, the O rescale skipped unless a row max grows by
 // more than 2^8, P packed to bf16 with v_cvt_pk_bf16_f32 and summed from the
 // packed pairs with v_dot2_f32_bf16, the row max exchanged between the two
@@ -330,20 +331,29 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
     return limit - tile * kKeys - 4 * half;
   };
   // Max of the raw scores of quarter q (key block q/2, entries 8(q%2) .. +7).
-  auto quarter_max = [&](const f32x16_t (&s)[2], int q, int rel, int ok, float mx, auto masked)
+  // On a tile that needs the per-key tests, the scores of keys the row may
+  // not see become -inf here, in place: the exponentials then need no tests
+  // (exp2(-inf) = 0, the scale being positive and finite).
+  auto quarter_max = [&](f32x16_t (&s)[2], int q, int rel, int ok, float mx, auto masked)
       __attribute__((always_inline)) {
 #pragma unroll
-    for (int e = 8 * (q & 1); e < 8 * (q & 1) + 8; ++e)
-      if (visible(rel, ok, q >> 1, e, masked)) mx = fmaxf(mx, s[q >> 1][e]);
+    for (int e = 8 * (q & 1); e < 8 * (q & 1) + 8; ++e) {
+      if constexpr (decltype(masked)::value)
+        s[q >> 1][e] = visible(rel, ok, q >> 1, e, masked) ? s[q >> 1][e] : -INFINITY;
+      mx = fmaxf(mx, s[q >> 1][e]);
+    }
     return mx;
   };
   // The same with the tile's two key blocks held in separate arrays.
-  auto quarter_max2 = [&](const f32x16_t& s0, const f32x16_t& s1, int q, int rel, int ok,
+  auto quarter_max2 = [&](f32x16_t& s0, f32x16_t& s1, int q, int rel, int ok,
                           float mx, auto masked) __attribute__((always_inline)) {
-    const f32x16_t& s = (q >> 1) ? s1 : s0;
+    f32x16_t& s = (q >> 1) ? s1 : s0;
 #pragma unroll
-    for (int e = 8 * (q & 1); e < 8 * (q & 1) + 8; ++e)
-      if (visible(rel, ok, q >> 1, e, masked)) mx = fmaxf(mx, s[e]);
+    for (int e = 8 * (q & 1); e < 8 * (q & 1) + 8; ++e) {
+      if constexpr (decltype(masked)::value)
+        s[e] = visible(rel, ok, q >> 1, e, masked) ? s[e] : -INFINITY;
+      mx = fmaxf(mx, s[e]);
+    }
     return mx;
   };
   // Folds a tile's row max (this lane's 32 keys and lane l^32's; the raw
@@ -373,13 +383,11 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   // Exponent pair i (0..15) of a tile: p = exp2(S scale - m_run) for entries
   // 2(i%8), +1 of key block i/8, packed to a bf16 pair in S^T accumulator
   // order and added (as rounded) into `sum`.
-  auto exp_pair = [&](const f32x16_t (&s)[2], int i, int rel, int ok, auto masked,
-                      uint32_t (&pw)[2][8], float& sum) __attribute__((always_inline)) {
+  auto exp_pair = [&](const f32x16_t (&s)[2], int i, uint32_t (&pw)[2][8], float& sum)
+      __attribute__((always_inline)) {
     const int kb = i >> 3, e = 2 * (i & 7);
-    const float p0 = visible(rel, ok, kb, e, masked)
-                         ? fast_exp2(fmaf(s[kb][e], a.scale_log2, -m_run)) : 0.f;
-    const float p1 = visible(rel, ok, kb, e + 1, masked)
-                         ? fast_exp2(fmaf(s[kb][e + 1], a.scale_log2, -m_run)) : 0.f;
+    const float p0 = fast_exp2(fmaf(s[kb][e], a.scale_log2, -m_run));
+    const float p1 = fast_exp2(fmaf(s[kb][e + 1], a.scale_log2, -m_run));
     pw[kb][e >> 1] = pack_bf16(p0, p1);
     sum = dot2_bf16(pw[kb][e >> 1], ones, sum);
   };
@@ -416,12 +424,14 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   //      j+1;
   // each with its LDS operand read three MFMAs ahead; then it folds the row
   // max into m_run, moves s_b1 into s_cur[1], waits for its loads and ends
-  // on the barrier.  mc / mn: whether tiles j / j+1 need the per-key tests.
+  // on the barrier.  mn: whether tile j+1 needs the per-key tests (its row
+  // max then also sets the scores of hidden keys to -inf, so tile j's
+  // exponentials, one step later, run without tests).
   f32x16_t s_cur[2];
   int ok_cur = 0;
   Pages pages_v{0, 0};
   RawIds raw_k{};
-  auto step = [&](int j, auto mc, auto mn, auto has_next) __attribute__((always_inline)) {
+  auto step = [&](int j, auto mn, auto has_next) __attribute__((always_inline)) {
     constexpr bool kNext = decltype(has_next)::value;
     // The ids of tile j+2 (loaded last step) are read before this step
     // issues any load.
@@ -436,7 +446,6 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
     uint32_t pw[2][8];
     f32x16_t s_b1;  // tile j+1's scores, key block 1
     {
-      const int rel = rel_of(j);
       float sum0 = 0.f, sum1 = 0.f;
       if constexpr (kNext) {
         const KTile& kb = ktiles[(j + 1) & 1];
@@ -456,12 +465,12 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
           else
             s_cur[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[i], qb[mi(i) >> 1],
                                                               i == 8 ? zero : s_cur[0], 0, 0, 0);
-          exp_pair(s_cur, i, rel, ok_cur, mc, pw, (i & 1) ? sum1 : sum0);
+          exp_pair(s_cur, i, pw, (i & 1) ? sum1 : sum0);
           __builtin_amdgcn_sched_barrier(0);
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) exp_pair(s_cur, i, rel, ok_cur, mc, pw, (i & 1) ? sum1 : sum0);
+        for (int i = 0; i < 16; ++i) exp_pair(s_cur, i, pw, (i & 1) ? sum1 : sum0);
       }
       l_half += sum0 + sum1;
     }
@@ -521,14 +530,13 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
     using F = std::false_type;
     using T = std::true_type;
     // Interior steps while tiles j and j+1 are interior and their pages all
-    // present, then one step into the masked tiles, then masked steps (a
-    // missing page, an error case, sends the rest down the masked path).
+    // present, then steps whose next tile is masked (a missing page, an
+    // error case, sends the rest down the masked path).
     const int last = ntiles - 1;
     int j = 0;
-    for (; j + 1 < n_full && (ok_cur & pages_v.ok) == 0xF; ++j) step(j, F{}, F{}, T{});
-    if (j < n_full && j < last && ok_cur == 0xF) step(j++, F{}, T{}, T{});
-    for (; j < last; ++j) step(j, T{}, T{}, T{});
-    step(last, T{}, T{}, F{});
+    for (; j + 1 < n_full && (ok_cur & pages_v.ok) == 0xF; ++j) step(j, F{}, T{});
+    for (; j < last; ++j) step(j, T{}, T{});
+    step(last, T{}, F{});
   }
 
   if (!row_ok) return;
@@ -654,7 +662,8 @@ extern "C" int kvc_batch_prefill_run(const kvc_prefill_schedule* sched, const in
               "cache blocks 4 GiB or more apart");
   KVC_REQUIRE(q_token_stride >= int64_t(Hq) * kD && out_token_stride >= int64_t(Hq) * kD,
               KVC_ERR_INVALID_ARG, "q/out token stride smaller than Hq*head_dim");
-  KVC_REQUIRE(sm_scale > 0.f, KVC_ERR_INVALID_ARG, "sm_scale must be positive");
+  KVC_REQUIRE(sm_scale > 0.f && std::isfinite(sm_scale), KVC_ERR_INVALID_ARG,
+              "sm_scale must be positive and finite");
   KVC_REQUIRE(aligned(q, 16) && aligned(key_cache, 16) && aligned(value_cache, 16) &&
                   aligned(out, 8) && aligned(plan, 16) && q_token_stride % 8 == 0 &&
                   out_token_stride % 4 == 0 && cache_block_stride % 8 == 0 &&

@@ -191,3 +191,16 @@ def test_prefill_at_the_bench_shape(gpu, kv_len):
             qb, k, v, attn_mask=causal_lower_right(2048, kv_len))
         assert_attn_close(out[qo[b]:qo[b + 1]].float().cpu().numpy(),
                           ref.permute(1, 0, 2).cpu().numpy())
+
+
+def test_prefill_rejects_a_non_finite_scale(gpu):
+    """Hidden keys are masked as -inf scores, which stays exact only for a
+    positive, finite scale: run() refuses any other."""
+    q, kc, vc, qo, kvi, idx, lpl = _case([5], [20], 32, 8, 39, device=gpu)
+    for bad in (float("inf"), 0.0, -1.0):
+        w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(WS, dtype=torch.uint8, device=gpu))
+        w.plan(torch.from_numpy(qo), torch.from_numpy(kvi), torch.from_numpy(idx).to(gpu),
+               torch.from_numpy(lpl), num_qo_heads=32, num_kv_heads=8, head_dim_qk=128,
+               page_size=16, causal=True, q_data_type=torch.bfloat16, sm_scale=bad)
+        with pytest.raises(RuntimeError, match="positive and finite"):
+            w.run(q, (kc.to(gpu), vc.to(gpu)))
