@@ -569,7 +569,9 @@ class PagedKVCache:
         ``decode`` calls after ``prepare_decode_step`` can be replayed after
         later ``prepare_decode_step`` calls while this key stays the same (the
         kernels read the new plan, lengths and page ids from the same
-        buffers); when it changes, capture again."""
+        buffers); when it changes, capture again and drop the old graph: its
+        launches address a step buffer that may have been freed.  An empty
+        key means the current plan is not a decode step's."""
         w = self._decode_wrapper
         s = w.schedule
         if (s is None or self._step_dev is None or self._step_slots is None
