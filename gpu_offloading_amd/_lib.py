@@ -74,6 +74,26 @@ class KvcPrefillSchedule(ctypes.Structure):
     ]
 
 
+class KvcDecodeStepLayout(ctypes.Structure):
+    """Mirror of ``kvc_decode_step_layout`` (include/kvc.h)."""
+
+    _fields_ = [
+        ("plan_ints", c_int64),
+        ("tail_begin", c_int64),
+        ("tail_end", c_int64),
+        ("ids", c_int64),
+        ("positions", c_int64),
+        ("indptr", c_int64),
+        ("lens_after", c_int64),
+        ("bt_pos", c_int64),
+        ("bt_val", c_int64),
+        ("num_reqs", c_int32),
+        ("num_bt_writes", c_int32),
+        ("max_seqs", c_int32),
+        ("block_size", c_int32),
+    ]
+
+
 _P = c_void_p
 _I32P = c_void_p  # device int32 pointers are passed as raw addresses
 # name -> (restype, argtypes).  Every entry point of include/kvc.h is listed;
@@ -140,6 +160,9 @@ SIGNATURES = {
     "kvc_copy_page_indices": (c_int, [
         _I32P, c_int64, c_int32, _I32P, _I32P, c_int32, c_int32, _I32P, c_int64, _P]),
     "kvc_stage_from_host": (c_int, [_I32P, _I32P, c_int64, c_int64, c_int64, _P]),
+    "kvc_decode_step_setup": (c_int, [
+        _I32P, _I32P, POINTER(KvcDecodeStepLayout), _I32P, c_int64, c_int32, c_int32,
+        _I32P, _P, c_int32, _I32P, c_int64, _P]),
 }
 
 _lock = threading.Lock()

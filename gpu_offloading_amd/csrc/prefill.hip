@@ -210,7 +210,9 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   // inline assembly so that the compiler does not make every later LDS read
   // wait for them (it cannot tell the buffer being filled from the one being
   // read); the step waits for them itself (vmcnt 0) before the barrier that
-  // publishes the tiles.  No compiler-generated code here uses M0.
+  // publishes the tiles.  No compiler-generated code here uses M0 (M0 is a
+  // reserved register hipcc will not take as a clobber;
+  // tests/test_prefill_m0.py checks the built assembly for any other use).
   auto lds_addr = [](const void* p) __attribute__((always_inline)) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t*)p));
   };

@@ -66,15 +66,22 @@ class BatchDecodeWithPagedKVCacheWrapper:
         self._indices_buf = paged_kv_indices_buffer
         self._lpl_buf = paged_kv_last_page_len_buffer
         self._segments_hint = int(num_segments or 0)
+        self._dev_index = self._device.index if self._device.index is not None \
+            else torch.cuda.current_device()
         self._num_cus = torch.cuda.get_device_properties(self._device).multi_processor_count
         self._sched: Optional[_lib.KvcDecodeSchedule] = None
         self._indices = None
         self._num_indices = 0
         self._sm_scale = None
         self._plan_args = None
-        # (id(k), id(v)) -> (k ref, v ref, (ps, hkv, d), k geometry, v geometry)
+        # (id(k), id(v)) -> (k ref, v ref, (ps, hkv, d), launch arguments)
         # for the cache tensors already checked (one pair per layer).
         self._kv_checked: dict = {}
+        self._fused_ok = False
+        self._cap_cache: dict = {}   # batch -> plan-image capacity
+        ws = float_workspace_buffer
+        self._ws_args = (ws.data_ptr(), ws.numel() * ws.element_size())
+        self._meta_refs = None   # the tensors _meta_args was made from
 
     # ------------------------------------------------------------------ plan
     def plan(self, indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
@@ -176,35 +183,62 @@ class BatchDecodeWithPagedKVCacheWrapper:
         if not indices_dev.is_contiguous():
             indices_dev = indices_dev.contiguous()
 
+        self._adopt(sched, plan_dev, indptr_dev, lpl_dev, indices_dev,
+                    float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(head_dim),
+                    (batch, num_qo_heads, num_kv_heads, head_dim, page_size))
+
+    begin_forward = plan
+
+    def _adopt(self, sched, plan_dev, indptr_dev, lpl_dev, indices_dev, sm_scale, plan_args):
+        """Make a staged schedule current and precompute the parts of the
+        launch arguments that stay fixed until the next plan."""
         self._sched = sched
         self._plan_dev = plan_dev
         self._indptr = indptr_dev
         self._lpl = lpl_dev
         self._indices = indices_dev
         self._num_indices = indices_dev.numel()
-        self._sm_scale = float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(head_dim)
-        self._plan_args = (batch, num_qo_heads, num_kv_heads, head_dim, page_size)
-
-    begin_forward = plan
+        self._sm_scale = sm_scale
+        self._plan_args = plan_args
+        self._pre_args = (sched, plan_dev.data_ptr())
+        r = self._meta_refs
+        if r is None or r[0] is not indptr_dev or r[1] is not indices_dev or r[2] is not lpl_dev:
+            self._meta_refs = (indptr_dev, indices_dev, lpl_dev)
+            self._meta_args = (indptr_dev.data_ptr(), indices_dev.data_ptr(),
+                               self._num_indices, lpl_dev.data_ptr())
+        self._fused_ok = (sched.head_dim == 128 and
+                          (sched.small_batch == 1 or
+                           (sched.heads_per_group == 8 and sched.append_pieces <= 4)))
 
     # ------------------------------------------------- in-package fast path
     def _plan_capacity(self, batch: int) -> int:
         """int32 entries to reserve for the plan image (16-byte multiple)."""
-        cap = _lib.load().kvc_decode_plan_ints(batch, max(self._segments_hint, 8 * self._num_cus))
-        return (cap + 3) // 4 * 4
+        cap = self._cap_cache.get(batch)
+        if cap is None:
+            cap = _lib.load().kvc_decode_plan_ints(batch,
+                                                   max(self._segments_hint, 8 * self._num_cus))
+            cap = (cap + 3) // 4 * 4
+            if len(self._cap_cache) > 4096:
+                self._cap_cache.clear()
+            self._cap_cache[batch] = cap
+        return cap
 
     def _schedule_into(self, indptr_host: np.ndarray, lpl_host: np.ndarray, batch: int,
                        num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
-                       image: torch.Tensor) -> _lib.KvcDecodeSchedule:
-        """kvc_decode_plan into the pinned int32 ``image``.  If the image is
-        too small, the returned schedule's ``plan_ints`` exceeds
-        ``image.numel()`` and nothing is staged: retry with a larger one."""
+                       image) -> _lib.KvcDecodeSchedule:
+        """kvc_decode_plan into the int32 ``image`` (a pinned tensor or a
+        numpy view of one).  If the image is too small, the returned
+        schedule's ``plan_ints`` exceeds its size and nothing is staged:
+        retry with a larger one."""
+        if isinstance(image, np.ndarray):
+            ptr, size = image.ctypes.data, image.size
+        else:
+            ptr, size = image.data_ptr(), image.numel()
         sched = _lib.KvcDecodeSchedule()
         st = _lib.load().kvc_decode_plan(indptr_host.ctypes.data, lpl_host.ctypes.data, batch,
                                          num_qo_heads, num_kv_heads, head_dim, page_size,
-                                         self._segments_hint, self._num_cus, sched,
-                                         image.data_ptr(), image.numel())
-        if st == _lib.KVC_ERR_WORKSPACE and sched.plan_ints > image.numel():
+                                         self._segments_hint, self._num_cus, sched, ptr, size)
+        if st == _lib.KVC_ERR_WORKSPACE and sched.plan_ints > size:
             return sched
         _lib.check("kvc_decode_plan", st)
         ws = self._workspace.numel() * self._workspace.element_size()
@@ -217,14 +251,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
                  num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int) -> None:
         """Adopt a schedule whose image and metadata are already on the device
         (staged by the caller in stream order before the next ``run``)."""
-        self._sched = sched
-        self._plan_dev = plan_dev
-        self._indptr = indptr_dev
-        self._lpl = lpl_dev
-        self._indices = indices_dev
-        self._num_indices = indices_dev.numel()
-        self._sm_scale = 1.0 / math.sqrt(head_dim)
-        self._plan_args = (sched.batch, num_qo_heads, num_kv_heads, head_dim, page_size)
+        self._adopt(sched, plan_dev, indptr_dev, lpl_dev, indices_dev, 1.0 / math.sqrt(head_dim),
+                    (sched.batch, num_qo_heads, num_kv_heads, head_dim, page_size))
 
     @property
     def schedule(self) -> _lib.KvcDecodeSchedule:
@@ -245,20 +273,11 @@ class BatchDecodeWithPagedKVCacheWrapper:
         (bf16 ``[B, num_qo_heads, head_dim]``) or ``(out, lse)``; lse is the
         natural-log log-sum-exp of the scaled logits.
         """
-        if any(s not in (None, 1.0) for s in (q_scale, k_scale, v_scale)):
+        if q_scale not in (None, 1.0) or k_scale not in (None, 1.0) or v_scale not in (None, 1.0):
             _fail("q/k/v scales are not supported (bf16 cache)")
-        k_cache, v_cache, out, lse = self._run_args(q, paged_kv_cache, out, lse, return_lse)
         sh = (stream.cuda_stream if stream is not None
               else _lib.current_stream_handle(self._device))
-        ws = self._workspace
-        _lib.call("kvc_batch_decode_run", self._sched, self._plan_dev.data_ptr(),
-                  q.data_ptr(), q.stride(0),
-                  k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
-                  k_cache.shape[0], self._indptr.data_ptr(), self._indices.data_ptr(),
-                  self._num_indices, self._lpl.data_ptr(), self._sm_scale, ws.data_ptr(),
-                  ws.numel() * ws.element_size(), out.data_ptr(), out.stride(0),
-                  lse.data_ptr() if lse is not None else None, sh)
-        return (out, lse) if return_lse else out
+        return self._launch(q, paged_kv_cache, out, lse, return_lse, sh, None, None)
 
     forward = run
 
@@ -267,9 +286,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
         """Whether ``run_with_append`` can serve the planned batch (head_dim
         128 and either a small-batch schedule or 8 KV heads per workgroup
         with few request ends per segment)."""
-        sc = self._sched
-        return (sc is not None and sc.head_dim == 128
-                and (sc.small_batch == 1 or (sc.heads_per_group == 8 and sc.append_pieces <= 4)))
+        return self._sched is not None and self._fused_ok
 
     def run_with_append(self, q: torch.Tensor,
                         paged_kv_cache: Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]],
@@ -282,34 +299,73 @@ class BatchDecodeWithPagedKVCacheWrapper:
         in the same launch (``kvc_batch_decode_append_run``).  Cache and
         output equal ``reshape_and_cache_flash`` followed by ``run`` bit for
         bit.  Raises unless ``fused_append_supported``."""
-        if not self.fused_append_supported:
-            _fail("the fused append needs head_dim 128, num_kv_heads a multiple of 8, "
-                  "group <= 4 and at most 4 request ends in a segment's leading pieces")
-        k_cache, v_cache, out, lse = self._run_args(q, paged_kv_cache, out, lse, return_lse)
-        batch, hq, hkv, d, ps = self._plan_args
-        for name, t in (("new_key", new_key), ("new_value", new_value)):
-            if (t.dtype != torch.bfloat16 or t.dim() != 3 or t.shape[0] < batch
-                    or tuple(t.shape[1:]) != (hkv, d) or t.stride(2) != 1 or t.stride(1) != d):
-                _fail(f"{name} must be bfloat16 [B, {hkv}, {d}] with contiguous heads")
-            if t.device != self._device:
-                _fail(f"{name} on a different device than the workspace")
         sh = (stream.cuda_stream if stream is not None
               else _lib.current_stream_handle(self._device))
-        ws = self._workspace
-        _lib.call("kvc_batch_decode_append_run", self._sched, self._plan_dev.data_ptr(),
-                  q.data_ptr(), q.stride(0),
-                  k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
-                  k_cache.shape[0], self._indptr.data_ptr(), self._indices.data_ptr(),
-                  self._num_indices, self._lpl.data_ptr(), new_key.data_ptr(), new_key.stride(0),
-                  new_value.data_ptr(), new_value.stride(0), self._sm_scale, ws.data_ptr(),
-                  ws.numel() * ws.element_size(), out.data_ptr(), out.stride(0),
-                  lse.data_ptr() if lse is not None else None, sh)
-        return (out, lse) if return_lse else out
+        return self._launch(q, paged_kv_cache, out, lse, return_lse, sh, new_key, new_value)
 
-    def _run_args(self, q, paged_kv_cache, out, lse, return_lse):
-        """Check run()'s tensors against the plan; allocate out / lse."""
+    def _launch(self, q, paged_kv_cache, out, lse, return_lse, sh, new_key, new_value,
+                kv=None):
+        """Check the call's tensors against the plan and launch the decode
+        (with the fused append when ``new_key`` is given) on stream ``sh``.
+        The plan's and the cache's arguments were checked and converted once
+        (``_adopt``, ``_kv_args``); per call only q, out, lse and the new rows
+        are checked.  ``kv``: the cache's launch arguments, already checked
+        (``PagedKVCache`` passes those of its own layers)."""
         if self._sched is None:
             _fail("run() called before plan()")
+        if kv is None:
+            kv = self._kv_args(paged_kv_cache)
+        batch, hq, hkv, d, ps = self._plan_args
+        dev = self._dev_index
+        qs, qt = q.shape, q.stride()
+        if (len(qs) != 3 or qs[0] < batch or qs[1] != hq or qs[2] != d
+                or q.dtype is not torch.bfloat16 or qt[2] != 1 or qt[1] != d):
+            _fail(f"q must be bfloat16 [{batch}, {hq}, {d}] with contiguous heads, "
+                  f"got {q.dtype} {tuple(qs)} strides {qt}")
+        if q.get_device() != dev:
+            _fail("q on a different device than the workspace")
+        if out is None:
+            out = torch.empty(batch, hq, d, dtype=torch.bfloat16, device=self._device)
+        else:
+            os_, ot = out.shape, out.stride()
+            if (len(os_) != 3 or os_[0] < batch or os_[1] != hq or os_[2] != d
+                    or out.dtype is not torch.bfloat16 or ot[2] != 1 or ot[1] != d
+                    or out.get_device() != dev):
+                _fail("out must be bfloat16 [B, num_qo_heads, head_dim] with contiguous heads "
+                      "on the workspace's device")
+        if return_lse and lse is None:
+            lse = torch.empty(batch, hq, dtype=torch.float32, device=self._device)
+        if lse is not None and (lse.dtype is not torch.float32 or not lse.is_contiguous()
+                                or lse.numel() < batch * hq or lse.get_device() != dev):
+            _fail("lse must be contiguous float32 [B, num_qo_heads] on the workspace's device")
+        lse_p = lse.data_ptr() if lse is not None else None
+        if new_key is None:
+            _lib.call("kvc_batch_decode_run", *self._pre_args, q.data_ptr(), qt[0], *kv,
+                      *self._meta_args, self._sm_scale, *self._ws_args, out.data_ptr(),
+                      out.stride(0), lse_p, sh)
+            return (out, lse) if return_lse else out
+        if not self._fused_ok:
+            _fail("the fused append needs head_dim 128, num_kv_heads a multiple of 8, "
+                  "group <= 4 and at most 4 request ends in a segment's leading pieces")
+        for name, t in (("new_key", new_key), ("new_value", new_value)):
+            ts, tt = t.shape, t.stride()
+            if (t.dtype is not torch.bfloat16 or len(ts) != 3 or ts[0] < batch
+                    or ts[1] != hkv or ts[2] != d or tt[2] != 1 or tt[1] != d):
+                _fail(f"{name} must be bfloat16 [B, {hkv}, {d}] with contiguous heads")
+            if t.get_device() != dev:
+                _fail(f"{name} on a different device than the workspace")
+        _lib.call("kvc_batch_decode_append_run", *self._pre_args, q.data_ptr(), qt[0], *kv,
+                  *self._meta_args, new_key.data_ptr(), new_key.stride(0), new_value.data_ptr(),
+                  new_value.stride(0), self._sm_scale, *self._ws_args, out.data_ptr(),
+                  out.stride(0), lse_p, sh)
+        return (out, lse) if return_lse else out
+
+    def _kv_args(self, paged_kv_cache):
+        """(k ptr, v ptr, block stride, token stride, blocks) of the cache
+        pair, checked against the plan's (page_size, heads, dim).  The
+        per-layer cache views are the same tensor objects call after call:
+        once checked they are recognised by identity, storage address and
+        block count."""
         batch, hq, hkv, d, ps = self._plan_args
         if isinstance(paged_kv_cache, (tuple, list)):
             k_cache, v_cache = paged_kv_cache
@@ -317,14 +373,12 @@ class BatchDecodeWithPagedKVCacheWrapper:
             if paged_kv_cache.dim() != 5 or paged_kv_cache.shape[1] != 2:
                 _fail("a single paged_kv_cache tensor must be [pages, 2, page_size, heads, dim]")
             k_cache, v_cache = paged_kv_cache[:, 0], paged_kv_cache[:, 1]
-        # The per-layer cache views are the same tensor objects call after
-        # call: once checked against this (page_size, heads, dim) they are
-        # only compared by identity, shape and strides.
         seen = self._kv_checked.get((id(k_cache), id(v_cache)))
         if (seen is not None and seen[0]() is k_cache and seen[1]() is v_cache
-                and seen[2] == (ps, hkv, d) and seen[3] == (k_cache.shape, k_cache.stride())
-                and seen[4] == (v_cache.shape, v_cache.stride())):
-            return k_cache, v_cache, *self._out_args(q, out, lse, return_lse)
+                and seen[2] == (ps, hkv, d) and seen[3][0] == k_cache.data_ptr()
+                and seen[3][4] == k_cache.shape[0] and seen[3][1] == v_cache.data_ptr()
+                and v_cache.shape[0] == seen[3][4]):
+            return seen[3]
         for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
             if c.dim() != 4 or tuple(c.shape[1:]) != (ps, hkv, d):
                 _fail(f"{name} must be [pages, {ps}, {hkv}, {d}], got {tuple(c.shape)}")
@@ -338,31 +392,11 @@ class BatchDecodeWithPagedKVCacheWrapper:
             _fail("k_cache and v_cache must share shape and strides")
         if len(self._kv_checked) >= 1024:
             self._kv_checked.clear()
+        kv = (k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
+              k_cache.shape[0])
         self._kv_checked[(id(k_cache), id(v_cache))] = (
-            weakref.ref(k_cache), weakref.ref(v_cache), (ps, hkv, d),
-            (k_cache.shape, k_cache.stride()), (v_cache.shape, v_cache.stride()))
-        return k_cache, v_cache, *self._out_args(q, out, lse, return_lse)
-
-    def _out_args(self, q, out, lse, return_lse):
-        """Check q against the plan; allocate or check out / lse."""
-        batch, hq, hkv, d, ps = self._plan_args
-        if q.dim() != 3 or q.shape[0] < batch or tuple(q.shape[1:]) != (hq, d):
-            _fail(f"q must be [{batch}, {hq}, {d}], got {tuple(q.shape)}")
-        if q.dtype != torch.bfloat16 or q.stride(2) != 1 or q.stride(1) != d:
-            _fail("q must be bfloat16 with contiguous heads")
-        if q.device != self._device:
-            _fail("q on a different device than the workspace")
-        if out is None:
-            out = torch.empty(batch, hq, d, dtype=torch.bfloat16, device=self._device)
-        elif (out.dtype != torch.bfloat16 or out.dim() != 3 or out.shape[0] < batch
-              or tuple(out.shape[1:]) != (hq, d) or out.stride(2) != 1 or out.stride(1) != d):
-            _fail("out must be bfloat16 [B, num_qo_heads, head_dim] with contiguous heads")
-        if return_lse and lse is None:
-            lse = torch.empty(batch, hq, dtype=torch.float32, device=self._device)
-        if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()
-                                or lse.numel() < batch * hq):
-            _fail("lse must be contiguous float32 [B, num_qo_heads]")
-        return out, lse
+            weakref.ref(k_cache), weakref.ref(v_cache), (ps, hkv, d), kv)
+        return kv
 
     def end_forward(self) -> None:
         """No-op kept for interface parity."""

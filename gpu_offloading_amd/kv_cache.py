@@ -16,6 +16,7 @@ small H2D copies of metadata, and stream/event ordering.
 """
 from __future__ import annotations
 
+import collections
 import math
 from dataclasses import dataclass, field
 from typing import Iterable, Optional, Sequence
@@ -23,7 +24,7 @@ from typing import Iterable, Optional, Sequence
 import numpy as np
 import torch
 
-from . import ops
+from . import _lib, hostmem, ops
 from .allocator import PagePool, pages_needed
 from .decode import BatchDecodeWithPagedKVCacheWrapper
 from .prefill import BatchPrefillWithPagedKVCacheWrapper
@@ -112,6 +113,10 @@ class PagedKVCache:
                                      dtype=dtype, device=self.device) for _ in range(num_layers)]
         self.k_cache = [t[:, 0] for t in self.kv_cache]
         self.v_cache = [t[:, 1] for t in self.kv_cache]
+        # Each layer's cache arguments of a decode launch (pointers, block and
+        # token strides, blocks): fixed for the cache's life.
+        self._layer_kv = [(k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.shape[0])
+                          for k, v in zip(self.k_cache, self.v_cache)]
 
         if self._dynamic_pages:
             self._bt = torch.full((max_seqs, self.max_pages_per_seq), -1,
@@ -125,8 +130,17 @@ class PagedKVCache:
         self._bt_pending: dict[int, int] = {}
         # slots of the step set up by prepare_decode_step (append_and_decode)
         self._step_slots: Optional[torch.Tensor] = None
-        # device copy of a decode step's metadata image (reused every step)
+        # device copy of a decode step's metadata image (reused every step),
+        # its slot mapping, and the streams that read them since the last
+        # upload (handle -> stream; the next upload waits for each)
         self._step_dev: Optional[torch.Tensor] = None
+        self._slots_dev: Optional[torch.Tensor] = None
+        self._step_views = None
+        self._step_layout = _lib.KvcDecodeStepLayout()
+        self._step_handle: Optional[int] = None
+        self._step_stream_obj = None
+        self._step_users: dict = {}
+        self._mixed_step_buf: Optional[torch.Tensor] = None
         self.seq_lens = torch.zeros(max_seqs, dtype=torch.int32, device=self.device)
         self._seq_lens_cpu = torch.zeros(max_seqs, dtype=torch.int32)
         self._pool = PagePool(self.total_pages, max_seqs, self.max_pages_per_seq,
@@ -142,8 +156,9 @@ class PagedKVCache:
         # pinned tensor per step costs a host allocation (and a wait) whenever
         # the host runs ahead of the GPU, as it does when the layers are
         # replayed from a graph.  Each slot: [buffer, event of its last copy].
-        self._meta_ring: list[list] = [[None, None] for _ in range(4)]
-        self._meta_next = 0
+        self._meta_ring: list[list] = [[None, None] for _ in range(self._META_RING)]
+        self._meta_step = 0
+        self._meta_events: collections.deque = collections.deque()
 
         self._staging_bytes = staging_bytes
         self._staging: Optional[torch.Tensor] = None
@@ -332,8 +347,9 @@ class PagedKVCache:
         block table (a negative id would wrap in numpy indexing, and a
         repeated one could size the page list past its device buffer)."""
         ids = np.asarray(seq_ids, dtype=np.int64).reshape(-1)
-        if len(ids) and (ids.min() < 0 or ids.max() >= self.max_seqs
-                         or len(np.unique(ids)) != len(ids)):
+        n = len(ids)
+        if n and (ids.min() < 0 or ids.max() >= self.max_seqs
+                  or (n > 1 and (len(set(ids.tolist())) if n <= 64 else len(np.unique(ids))) != n)):
             raise ValueError(f"seq_ids must be distinct and in [0, {self.max_seqs})")
         return ids
 
@@ -459,6 +475,7 @@ class PagedKVCache:
         """Causal attention of the planned chunks' queries ``[sum(chunk), Hq, D]``
         over the paged cache of ``layer`` (moe_engine.py:3939-3941)."""
         self._require_gpu()
+        self._step_stream_for_call()
         return self._prefill_wrapper.run(q, (self.k_cache[layer], self.v_cache[layer]),
                                          out=out, return_lse=return_lse)
 
@@ -466,7 +483,17 @@ class PagedKVCache:
         """Setup of a pure-decode step in the engine's order
         (moe_engine.py:2655-2695, 3511-3556): slot mapping from the current
         lengths, then ``seq_lens += 1``, then plan.  Pages must already cover
-        the new token (the scheduler's ``ensure_pages``)."""
+        the new token (the scheduler's ``ensure_pages``).
+
+        The device work is one launch (``kvc_decode_step_setup``) on the
+        current stream.  The returned slot mapping (int64, -1 padded to
+        ``graph_n``) lives in a buffer the cache reuses: it holds this step's
+        slots until the next ``prepare_decode_step``, like the engine's static
+        slot-mapping buffer.  The step's metadata also lives in a reused
+        buffer; eager ``decode``/``append_and_decode`` calls on another stream
+        are ordered after this setup, and the next setup after them.  A
+        graph replay of the step's launches must run on this call's stream
+        (or the caller orders the streams)."""
         self._require_gpu()
         b = len(seq_ids)
         graph_n = b if graph_n is None else graph_n
@@ -489,78 +516,119 @@ class PagedKVCache:
                 raise RuntimeError(f"sequences {short} have no page for the new token "
                                    "(ensure_pages first)")
 
-        # One pinned int32 image of the step's metadata, one upload into the
-        # cache's step buffer (the same device memory every step, so a decode
-        # launch captured in a graph reads the new plan when replayed):
-        #   decode schedule (cap, 16-byte aligned) | ids[b] | qsl[b+1]
-        #   | lens_before[ms] | lens_after[ms] | kv_indptr[b+1] | last_page_len[b]
+        # One pinned int32 image of the step's metadata, read by one setup
+        # kernel that also writes its device copy into the cache's step
+        # buffer (the same device memory every step, so a decode launch
+        # captured in a graph reads the new plan when replayed):
+        #   decode schedule (cap, 16-byte aligned) | ids[b] | positions[b]
+        #   | kv_indptr[b+1] | last_page_len[b] | lens_after[ms]
         #   | block-table positions (int64) | page ids
         pend = self._peek_bt_pending()
         u = 0 if pend is None else len(pend[0])
         w = self._decode_wrapper
         cap = w._plan_capacity(b)
         while True:
-            o_plan = 0
             o_ids = cap
-            o_qsl = o_ids + b
-            o_lb = o_qsl + b + 1
-            o_la = o_lb + ms
-            o_ip = o_la + ms
+            o_pos = o_ids + b
+            o_ip = o_pos + b
             o_lpl = o_ip + b + 1
-            o_pos = (o_lpl + b + 1) // 2 * 2
-            o_val = o_pos + 2 * u
-            n = o_val + u
-            hs = self._host_image(n)
-            h = hs.numpy()
-            h[o_ids:o_qsl] = ids
-            h[o_qsl:o_lb] = np.arange(b + 1, dtype=np.int32)
-            h[o_lb:o_la] = lens_all
-            h[o_la:o_ip] = lens_all
-            h[o_la + ids] += 1
+            o_la = o_lpl + b
+            o_bpos = (o_la + ms + 1) // 2 * 2
+            o_bval = o_bpos + 2 * u
+            n = o_bval + u
+            hs, h = self._host_image_np(n)
+            h[o_ids:o_pos] = ids
+            h[o_pos:o_ip] = lens_all[ids]
             nblk = (lens + ps - 1) // ps
             h[o_ip] = 0
             np.cumsum(nblk, out=h[o_ip + 1:o_ip + b + 1])
-            lpl = lens % ps
-            h[o_lpl:o_lpl + b] = np.where(lpl == 0, ps, lpl)
+            h[o_lpl:o_lpl + b] = (lens - 1) % ps + 1     # lens >= 1
+            h[o_la:o_la + ms] = lens_all
+            h[o_la + ids] += 1
             if u:
-                h[o_pos:o_pos + 2 * u].view(np.int64)[:] = pend[0]
-                h[o_val:o_val + u] = pend[1]
+                h[o_bpos:o_bpos + 2 * u].view(np.int64)[:] = pend[0]
+                h[o_bval:o_bval + u] = pend[1]
             sched = w._schedule_into(h[o_ip:o_ip + b + 1], h[o_lpl:o_lpl + b], b,
                                      self.num_heads, self.num_kv_heads, self.head_dim, ps,
-                                     hs[o_plan:o_plan + cap])
+                                     h[0:cap])
             if sched.plan_ints <= cap:
                 break
             cap = (sched.plan_ints + 3) // 4 * 4
-        total = int(h[o_ip + b])
 
+        sh = self._claim_step_buffer()
+        self._mixed_step_buf = None
         if self._step_dev is None or self._step_dev.numel() < n:
             # grows rarely (more requests or block-table writes than before);
             # a graph captured before must then be captured again
             self._step_dev = torch.empty(2 * max(n, 0 if self._step_dev is None
                                                  else self._step_dev.numel()),
                                          dtype=torch.int32, device=self.device)
-        dm = self._step_dev[:n]
-        # The plan's unused capacity is not sent.
-        ops.stage_from_host(hs, dm, int(sched.plan_ints), cap, n)
+        if self._slots_dev is None or self._slots_dev.numel() < graph_n:
+            self._slots_dev = torch.empty(2 * graph_n, dtype=torch.int64, device=self.device)
+        # Views of the step buffers, made again only when a shape changes.
+        vk = (self._step_dev.data_ptr(), self._slots_dev.data_ptr(), cap, b, graph_n)
+        if self._step_views is None or self._step_views[0] != vk:
+            dm = self._step_dev
+            self._step_views = (vk, dm[0:cap], dm[o_ip:o_lpl], dm[o_lpl:o_lpl + b],
+                                self._slots_dev[:graph_n], self._slots_dev[:b])
+        _, plan_v, indptr_v, lpl_v, slots, step_slots = self._step_views
+        lay = self._step_layout
+        lay.plan_ints = int(sched.plan_ints)   # the plan's unused capacity is not sent
+        lay.tail_begin, lay.tail_end = cap, n
+        lay.ids, lay.positions, lay.indptr, lay.lens_after = o_ids, o_pos, o_ip, o_la
+        lay.bt_pos, lay.bt_val = o_bpos, o_bval
+        lay.num_reqs, lay.num_bt_writes, lay.max_seqs, lay.block_size = b, u, ms, ps
+        ops.decode_step_setup(hs, self._step_dev, lay, self._bt, self.seq_lens, slots,
+                              self._plan_indices_gpu, stream_handle=sh)
         self._host_image_sent()
         if u:
-            self._bt.view(-1).scatter_(0, dm[o_pos:o_val].view(torch.int64), dm[o_val:o_val + u])
             self._bt_pending.clear()
-        ids_d = dm[o_ids:o_qsl]
-        slots = torch.empty(graph_n, dtype=torch.int64, device=self.device)
-        ops.compute_slot_mapping(self._bt, ids_d, dm[o_qsl:o_lb], dm[o_lb:o_la], b, slots,
-                                 block_size=ps)
-        self.seq_lens.copy_(dm[o_la:o_ip])
-        indptr_d = dm[o_ip:o_lpl]
-        ops.copy_page_indices(self._bt, indptr_d, self._plan_indices_gpu, seq_ids=ids_d)
         # The whole page-index buffer goes to the decode (its pages are bounded
         # by the plan), so the launch does not change with the page count.
-        w._install(sched, dm[o_plan:o_plan + cap], indptr_d, dm[o_lpl:o_lpl + b],
-                   self._plan_indices_gpu, self.num_heads, self.num_kv_heads,
-                   self.head_dim, ps)
+        w._install(sched, plan_v, indptr_v, lpl_v, self._plan_indices_gpu, self.num_heads,
+                   self.num_kv_heads, self.head_dim, ps)
         lens_all[ids] += 1
-        self._step_slots = slots[:b]
+        self._step_slots = step_slots
         return slots
+
+    # ------------------------------------------------- step-buffer streams
+    def _claim_step_buffer(self) -> int:
+        """Order the current stream after every other stream that used the
+        step buffer since its last upload, before it is rewritten; return the
+        current stream's handle, now the step's stream.  (Stream objects are
+        only made on the rare path where another stream was involved.)"""
+        sh = _lib.current_stream_handle(self.device)
+        if self._step_users:
+            cur = torch.cuda.current_stream(self.device)
+            for h, st in self._step_users.items():
+                if h != sh:
+                    cur.wait_stream(st)
+            self._step_users = {}
+        self._step_handle = sh
+        self._step_stream_obj = None
+        return sh
+
+    def _step_stream_for_call(self) -> int:
+        """Handle of the current stream for a launch that reads the step
+        buffer.  A stream other than the step's is first ordered after the
+        upload (eager calls only; under graph capture ordering is the
+        caller's) and remembered, so that the next upload waits for it."""
+        sh = _lib.current_stream_handle(self.device)
+        if sh != self._step_handle and self._step_handle is not None \
+                and sh not in self._step_users:
+            if torch.cuda.is_current_stream_capturing():
+                return sh
+            cur = torch.cuda.current_stream(self.device)
+            if self._step_stream_obj is None:
+                self._step_stream_obj = torch.cuda.ExternalStream(self._step_handle,
+                                                                  device=self.device)
+            cur.wait_stream(self._step_stream_obj)
+            self._step_users[sh] = cur
+            if self._mixed_step_buf is not None:
+                # a mixed step's buffer is freed at the next plan: keep the
+                # allocator from reusing it before this stream ran
+                self._mixed_step_buf.record_stream(cur)
+        return sh
 
     def decode_graph_key(self) -> tuple:
         """What a decode launch of the current step bakes in besides its
@@ -711,7 +779,9 @@ class PagedKVCache:
                                                 (c_after + ps - 1) // ps]))
 
         # The step's one upload; the plans' unused capacity is not sent.
+        self._claim_step_buffer()
         dm = torch.empty(hs.numel(), dtype=torch.int32, device=self.device)
+        self._mixed_step_buf = dm
         ops.stage_from_host(hs, dm, o_dplan + (int(dsched.plan_ints) if D else 0),
                             o_pplan, o_pplan + (int(psched.plan_ints) if C else 0))
         self._host_image_sent()
@@ -761,22 +831,26 @@ class PagedKVCache:
         ``key``/``value`` are the step's new rows ``[B, Hkv, D]`` in the order
         of that call's ``seq_ids``; the result is the same either way, bit for
         bit."""
-        self._require_gpu()
         slots = self._step_slots
         if slots is None:
+            self._require_gpu()
             raise RuntimeError("append_and_decode needs a prepare_decode_step first")
         w = self._decode_wrapper
-        if w.fused_append_supported:
-            return w.run_with_append(q, (self.k_cache[layer], self.v_cache[layer]), key, value,
-                                     out=out, return_lse=return_lse)
+        sh = self._step_stream_for_call()
+        kv = self._layer_kv[layer]
+        if w._fused_ok:
+            return w._launch(q, None, out, None, return_lse, sh, key, value, kv)
         self.append(layer, key, value, slots)
-        return self.decode(layer, q, out=out, return_lse=return_lse)
+        return w._launch(q, None, out, None, return_lse, sh, None, None, kv)
 
     def decode(self, layer: int, q: torch.Tensor, out: Optional[torch.Tensor] = None,
                return_lse: bool = False):
+        """Decode attention of the planned requests over ``layer`` (the
+        engine's FlashInfer run, moe_engine.py:3907-3909)."""
         self._require_gpu()
-        return self._decode_wrapper.run(q, (self.k_cache[layer], self.v_cache[layer]),
-                                        out=out, return_lse=return_lse)
+        return self._decode_wrapper._launch(q, None, out, None, return_lse,
+                                            self._step_stream_for_call(), None, None,
+                                            self._layer_kv[layer])
 
     def gather(self, layer: int, seq_ids: Sequence[int], out_key: Optional[torch.Tensor] = None,
                out_value: Optional[torch.Tensor] = None):
@@ -817,31 +891,71 @@ class PagedKVCache:
             self._copy_stream = torch.cuda.Stream(device=self.device)
         return self._copy_stream
 
-    def _host_image(self, n: int) -> torch.Tensor:
-        """A pinned int32 image of ``n`` entries for the step's metadata: the
-        ring's next slot, once the copy that last read it has run (the host
-        stays at most four steps ahead of the GPU)."""
-        slot = self._meta_ring[self._meta_next]
-        if slot[1] is not None:
-            slot[1].synchronize()
+    # The pinned step images form a ring of _META_RING slots, one per step.
+    # A slot is rewritten only after the kernel that read it last (R steps
+    # ago) has run.  Recording an event costs the host ~4 us, so one is
+    # recorded every _META_EVERY steps: before step t reuses its slot, the
+    # host waits for the first event recorded at or after step t - R, which
+    # exists (R >= _META_EVERY) and was recorded before step t.  Every step's
+    # upload runs after the previous steps' (each setup orders its stream
+    # after the streams that used the step buffer), so that event's
+    # completion covers step t - R.
+    _META_RING = 8
+    _META_EVERY = 4
+
+    def _meta_slot(self, n: int) -> list:
+        t = self._meta_step
+        slot = self._meta_ring[t % self._META_RING]
+        if t >= self._META_RING:
+            need = t - self._META_RING
+            ev = self._meta_events
+            while ev and ev[0][0] < need:
+                ev.popleft()
+            if ev and ev[0][0] < t:
+                ev[0][1].synchronize()
         if slot[0] is None or slot[0].numel() < n:
             slot[0] = torch.empty(max(n, 2 * (0 if slot[0] is None else slot[0].numel())),
                                   dtype=torch.int32, pin_memory=True)
-        return slot[0][:n]
+            slot[1] = slot[0].numpy()
+        return slot
+
+    def _host_image(self, n: int) -> torch.Tensor:
+        """A pinned int32 image of ``n`` entries for the step's metadata: the
+        ring's next slot, once the upload that last read it has run."""
+        return self._meta_slot(n)[0][:n]
+
+    def _host_image_np(self, n: int):
+        """``_host_image`` for the decode step: the ring slot's whole pinned
+        tensor (its first ``n`` entries are the image) and a numpy view of
+        those ``n`` entries (no per-step tensor view)."""
+        slot = self._meta_slot(n)
+        return slot[0], slot[1][:n]
 
     def _host_image_sent(self) -> None:
-        """Mark the slot ``_host_image`` returned as read by the copy just
+        """Mark the slot ``_host_image`` returned as read by the upload just
         issued on the current stream, and move to the next slot."""
-        slot = self._meta_ring[self._meta_next]
-        if slot[1] is None:
-            slot[1] = torch.cuda.Event()
-        slot[1].record()
-        self._meta_next = (self._meta_next + 1) % len(self._meta_ring)
+        t = self._meta_step
+        if t % self._META_EVERY == 0:
+            e = torch.cuda.Event()
+            e.record()
+            self._meta_events.append((t, e))
+        self._meta_step = t + 1
 
     def _staging_buf(self) -> torch.Tensor:
         if self._staging is None:
             self._staging = torch.empty(self._staging_bytes, dtype=torch.uint8, device=self.device)
         return self._staging
+
+    def reserve_swap(self) -> None:
+        """Allocate the swap staging buffer and create the side and DMA
+        streams now, so that the first ``swap_out`` does not pay for them on
+        the engine loop (a 512 MiB device allocation and two stream creations
+        take ~17 ms of host time).  Without this call they are made on the
+        first swap."""
+        self._require_gpu()
+        self._staging_buf()
+        self._side_stream()
+        self._dma_stream()
 
     def _staging_halves(self, per_block: int):
         """The staging buffer as two halves and the blocks one half holds."""
@@ -967,7 +1081,7 @@ class PagedKVCache:
         bb = ops.block_bytes(self.k_cache[0])
         nbytes = self.num_layers * n * 2 * bb
         if host is None:
-            host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+            host = hostmem.pinned_empty(nbytes, self.device)
         elif host.is_cuda or not host.is_pinned() or host.numel() * host.element_size() < nbytes:
             raise RuntimeError(f"host buffer must be pinned CPU memory of >= {nbytes} bytes")
         ids_t = self._to_device(np.asarray(ids, dtype=np.int32))

@@ -34,6 +34,7 @@ from typing import Dict, List, Optional, Sequence
 import numpy as np
 import torch
 
+from . import hostmem
 from .kv_cache import PagedKVCache, SwapHandle
 
 __all__ = ["SwapPreemption", "PagedOffloadKV", "KVOffloadPipeline"]
@@ -166,8 +167,12 @@ class PagedOffloadKV:
         dec_off, pre_off = self.decode_offload_blocks, self.prefill_offload_blocks
 
         def pinned(n, shape):
-            t = torch.zeros((n,) + shape, dtype=dtype)
-            return t.pin_memory() if self.device.type == "cuda" else t
+            if self.device.type != "cuda":
+                return torch.zeros((n,) + shape, dtype=dtype)
+            numel = n * math.prod(shape)
+            t = hostmem.pinned_empty(numel * dtype.itemsize,
+                                     self.device, dtype)
+            return t.zero_().view((n,) + shape)
 
         kshape, vshape = (h, d // x, bs, x), (h, d, bs)
         self.k_offload_cpu = [pinned(dec_off, kshape) for _ in range(num_layers - 1)]

@@ -313,6 +313,42 @@ def stage_from_host(host: torch.Tensor, dev: torch.Tensor, head: int,
     return dev
 
 
+def decode_step_setup(host: torch.Tensor, dev: torch.Tensor, layout,
+                      block_table: torch.Tensor, seq_lens: torch.Tensor,
+                      slot_mapping: torch.Tensor, indices: torch.Tensor, *,
+                      stream_handle: Optional[int] = None) -> None:
+    """A pure-decode step's whole device setup in one launch
+    (``kvc_decode_step_setup``): upload of the pinned int32 image ``host``
+    into ``dev``, the block-table writes it lists, ``seq_lens``, the new
+    tokens' slots (-1 padded to ``slot_mapping.numel()``) and the page-index
+    flatten into ``indices`` -- the engine's setup sequence
+    (moe_engine.py:3493-3556, 1937-1946).  ``layout`` is a
+    ``_lib.KvcDecodeStepLayout``; ``host`` must stay unchanged until the
+    kernel ran (record an event after the call).  The caller (the cache)
+    builds every tensor, so only what the kernel indexes by is checked."""
+    # (the library checks that host is pinned memory)
+    if host.is_cuda or host.dtype != torch.int32:
+        _fail("host must be a pinned int32 CPU tensor")
+    if not (dev.dtype == torch.int32 and block_table.dtype == torch.int32
+            and seq_lens.dtype == torch.int32 and indices.dtype == torch.int32
+            and slot_mapping.dtype == torch.int64):
+        _fail("dev, block_table, seq_lens and indices must be int32, slot_mapping int64")
+    if layout.tail_end > min(host.numel(), dev.numel()):
+        _fail("the layout's tail range does not fit the images")
+    if (block_table.stride(1) != 1 or block_table.stride(0) != block_table.shape[1]
+            or not (seq_lens.is_contiguous() and slot_mapping.is_contiguous()
+                    and indices.is_contiguous())):
+        _fail("block_table rows, seq_lens, slot_mapping and indices must be contiguous")
+    if seq_lens.numel() < layout.max_seqs or slot_mapping.numel() < layout.num_reqs:
+        _fail("seq_lens or slot_mapping too short for the layout")
+    sh = (stream_handle if stream_handle is not None
+          else _lib.current_stream_handle(dev.device))
+    _lib.call("kvc_decode_step_setup", host.data_ptr(), dev.data_ptr(), layout,
+              block_table.data_ptr(), block_table.stride(0), block_table.shape[0],
+              block_table.shape[1], seq_lens.data_ptr(), slot_mapping.data_ptr(),
+              slot_mapping.numel(), indices.data_ptr(), indices.numel(), sh)
+
+
 # --------------------------------------------------------------------------
 # (a10) block eviction / restore
 # --------------------------------------------------------------------------

@@ -441,6 +441,53 @@ int kvc_copy_page_indices(const int32_t* block_table,
 int kvc_stage_from_host(const int32_t* host, int32_t* dev, int64_t head,
                         int64_t tail_begin, int64_t tail_end, void* stream);
 
+/* kvc_decode_step_setup is the engine's whole pure-decode step setup in one
+ * launch: the pinned uploads (src/MoE/moe_engine.py:3493-3494, 3506-3507),
+ * the block-table writes the scheduler made since the last step, vLLM's
+ * prepare_pos_seq_lens + _compute_slot_mappings_kernel for one new token per
+ * request (:3514-3541), the device lengths (:3554-3556) and the page-index
+ * flatten of FlashInfer's plan (:1937-1946).  From the pinned int32
+ * host_image (layout below, offsets in int32 units):
+ *   dev_image[i] = host_image[i] for i in [0, plan_ints) and
+ *                  [tail_begin, tail_end)  (the decode plan and the fields);
+ *   block_table[p / max_pages_per_seq][p % max_pages_per_seq] = bt_val[k]
+ *       for the distinct int64 flat positions p = bt_pos[k], k < num_bt_writes
+ *       (positions outside the table are skipped);
+ *   seq_lens[i] = lens_after[i], i < max_seqs;
+ *   slot_mapping[r] = block_table[ids[r]][pos / bs] * bs + pos % bs with
+ *       pos = positions[r] (the new token's position), r < num_reqs, and -1
+ *       for r in [num_reqs, num_slots) and for rows or pages outside the table;
+ *   indices[indptr[r] + j] = block_table[ids[r]][j], j < indptr[r+1]-indptr[r]
+ *       (entries at or past indices_capacity are not written),
+ * every read of the table seeing the step's writes.  The fields are read
+ * from the image when the kernel runs: keep host_image unchanged until an
+ * event recorded after this call has completed.  host_image must be pinned
+ * (hipHostMalloc, torch pin_memory), both images 16-byte aligned, the
+ * block-table rows contiguous (flat positions count max_pages_per_seq per
+ * row).  Every field must lie in [tail_begin, tail_end). */
+typedef struct kvc_decode_step_layout {
+  int64_t plan_ints;    /* [0, plan_ints): the decode plan image            */
+  int64_t tail_begin;   /* [tail_begin, tail_end): the step's fields,       */
+  int64_t tail_end;     /*   tail_begin a multiple of 4                     */
+  int64_t ids;          /* int32[num_reqs]: block-table row of request r    */
+  int64_t positions;    /* int32[num_reqs]: position of its new token       */
+  int64_t indptr;       /* int32[num_reqs + 1]: page offsets                */
+  int64_t lens_after;   /* int32[max_seqs]: every row's length after it     */
+  int64_t bt_pos;       /* int64[num_bt_writes] (even offset): flat positions */
+  int64_t bt_val;       /* int32[num_bt_writes]: page ids written there     */
+  int32_t num_reqs;
+  int32_t num_bt_writes;
+  int32_t max_seqs;
+  int32_t block_size;
+} kvc_decode_step_layout;
+
+int kvc_decode_step_setup(const int32_t* host_image, int32_t* dev_image,
+                          const kvc_decode_step_layout* layout,
+                          int32_t* block_table, int64_t block_table_row_stride,
+                          int32_t block_table_rows, int32_t max_pages_per_seq,
+                          int32_t* seq_lens, int64_t* slot_mapping, int32_t num_slots,
+                          int32_t* indices, int64_t indices_capacity, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -199,6 +199,26 @@ def gather_kv(k_cache: np.ndarray, v_cache: np.ndarray, block_table: np.ndarray,
 # ----------------------------------------------------- decode attention
 
 
+def _request_kv(k_cache: np.ndarray, v_cache: np.ndarray, pages: np.ndarray, n: int):
+    """K and V (float32 ``[n, Hkv, D]``) of a request's first ``n`` tokens on
+    ``pages``, and which of them are present.  A page id outside
+    ``[0, num_blocks)`` (-1 for an unallocated block-table entry) is a missing
+    page: its tokens are hidden from the attention (their K/V rows read as 0
+    and they are masked out), the error behaviour this build's kernels define
+    for a corrupt page list (the engine never plans one; FlashInfer would read
+    out of bounds)."""
+    nb, ps = k_cache.shape[:2]
+    pages = np.asarray(pages, np.int64)
+    ok = (pages >= 0) & (pages < nb)
+    safe = np.where(ok, pages, 0)
+    present = np.repeat(ok, ps)[:n]
+    K = bf16_to_f32(k_cache[safe].reshape(-1, *k_cache.shape[2:])[:n])
+    V = bf16_to_f32(v_cache[safe].reshape(-1, *v_cache.shape[2:])[:n])
+    K[~present] = 0.0
+    V[~present] = 0.0
+    return K, V, present
+
+
 def paged_decode(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
                  indptr: np.ndarray, indices: np.ndarray, last_page_len: np.ndarray,
                  sm_scale: Optional[float] = None):
@@ -208,8 +228,9 @@ def paged_decode(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
     default sm_scale 1/sqrt(head_dim)):
         out[b, h] = softmax(sm_scale * q[b, h] . K_b^T) . V_b,  kv head = h // (Hq/Hkv)
     over the len_b = (pages-1)*ps + last_page_len[b] tokens of request b.
+    Tokens of missing pages (``_request_kv``) are hidden.
     q: bf16 bits [B, Hq, D]; returns (out float32 [B, Hq, D], lse float32 [B, Hq],
-    natural log; a request with no pages gives out 0, lse -inf)."""
+    natural log; a request with no (present) token gives out 0, lse -inf)."""
     q = bf16_to_f32(q)
     B, Hq, D = q.shape
     nb, ps, Hkv, _ = k_cache.shape
@@ -222,11 +243,13 @@ def paged_decode(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
         if len(pages) == 0:
             continue
         n = (len(pages) - 1) * ps + int(last_page_len[b])
-        K = bf16_to_f32(k_cache[pages].reshape(-1, Hkv, D)[:n])
-        V = bf16_to_f32(v_cache[pages].reshape(-1, Hkv, D)[:n])
+        K, V, present = _request_kv(k_cache, v_cache, pages, n)
+        if not present.any():
+            continue
         for h in range(Hkv):
             qg = q[b, h * G:(h + 1) * G]                      # [G, D]
             s = (qg @ K[:, h, :].T) * scale                  # [G, n]
+            s = np.where(present[None, :], s, -np.inf)
             m = s.max(axis=1, keepdims=True)
             p = np.exp(s - m)
             l = p.sum(axis=1, keepdims=True)
@@ -246,7 +269,8 @@ def paged_prefill(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
     Request b owns query rows qo_indptr[b]..qo_indptr[b+1] (q_len) and the
     kv_len = (pages-1)*ps + last_page_len[b] cached tokens of its pages; with
     causal masking query i sees keys j <= i + kv_len - q_len (the chunk is
-    the tail of the cache).  A query that sees nothing gives out 0, lse -inf.
+    the tail of the cache); tokens of missing pages (``_request_kv``) are
+    hidden.  A query that sees nothing gives out 0, lse -inf.
     q: bf16 bits [total_q, Hq, D]; returns (out float32, lse float32 natural log)."""
     q = bf16_to_f32(q)
     T, Hq, D = q.shape
@@ -262,11 +286,11 @@ def paged_prefill(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
             continue
         q_len = q1 - q0
         n = (len(pages) - 1) * ps + int(last_page_len[b])
-        K = bf16_to_f32(k_cache[pages].reshape(-1, Hkv, D)[:n])
-        V = bf16_to_f32(v_cache[pages].reshape(-1, Hkv, D)[:n])
+        K, V, present = _request_kv(k_cache, v_cache, pages, n)
         seen = np.ones((q_len, n), bool)
         if causal:
             seen = np.arange(n)[None, :] <= np.arange(q_len)[:, None] + (n - q_len)
+        seen &= present[None, :]
         any_seen = seen.any(axis=1)
         for h in range(Hkv):
             for g in range(G):

@@ -442,3 +442,31 @@ def test_a_library_built_from_other_sources_is_refused(tmp_path, monkeypatch):
     monkeypatch.setattr(build, "STAMP_PATH", str(tmp_path / "missing"))
     with pytest.raises(RuntimeError, match="no build stamp"):
         _lib._check_fresh()
+
+
+def test_struct_layouts_match_header(tmp_path):
+    """The ctypes mirrors of the header's structs have the C layout: every
+    field's offset and each struct's size, from a program compiled against
+    include/kvc.h with the host C compiler."""
+    mirrors = {"kvc_decode_schedule": _lib.KvcDecodeSchedule,
+               "kvc_prefill_schedule": _lib.KvcPrefillSchedule,
+               "kvc_decode_step_layout": _lib.KvcDecodeStepLayout}
+    lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "kvc.h"', 'int main(void) {']
+    for name, cls in mirrors.items():
+        lines.append(f'  printf("{name} size %zu\\n", sizeof({name}));')
+        for field, _ in cls._fields_:
+            lines.append(f'  printf("{name} {field} %zu\\n", offsetof({name}, {field}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", INCLUDE, str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                               check=True).stdout.splitlines():
+        struct, field, value = line.split()
+        got[(struct, field)] = int(value)
+    for name, cls in mirrors.items():
+        assert got[(name, "size")] == ctypes.sizeof(cls), name
+        for field, _ in cls._fields_:
+            assert got[(name, field)] == getattr(cls, field).offset, (name, field)

@@ -76,6 +76,35 @@ def test_decode_cfg1_vs_oracle_and_sdpa(gpu):
         assert np.allclose(lse.cpu().numpy(), ref_lse, atol=1e-3, rtol=1e-4)
 
 
+@pytest.mark.parametrize("d,lens", [(128, [300, 700, 64, 1000, 90]),   # streaming kernel
+                                     (128, [40, 100, 200]),              # small-batch kernel
+                                     (64, [300, 700, 64, 1000, 90])])    # register kernel
+def test_decode_missing_pages_are_hidden(gpu, d, lens):
+    """Page ids of -1 or past the cache hide their tokens (the oracle's
+    missing-page semantics); the blocks they used to name hold NaN bits and
+    must not leak; a request whose pages are all missing gives 0 / -inf."""
+    kc, vc, bt, indptr, indices, lpl = _paged(lens, 8, d, 70 + d + len(lens), device=gpu)
+    nb = kc.shape[0]
+    idx = indices.copy()
+    hidden = [int(idx[indptr[0] + 2]), int(idx[indptr[1] + 1])]
+    idx[indptr[0] + 2] = -1
+    idx[indptr[1] + 1] = nb + 3
+    idx[indptr[-2]:indptr[-1]] = -1
+    for p in hidden:
+        kc[p] = float("nan")
+        vc[p] = float("nan")
+    q = randn_bf16((len(lens), 32, d), 71 + d, device=gpu)
+    (out, lse), w = _run(gpu, q, kc, vc, indptr, idx, lpl, 32, 8, d)
+    ref, ref_lse = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, idx, lpl)
+    assert torch.isfinite(out).all()
+    assert_attn_close(out.float().cpu().numpy(), ref)
+    got = lse.cpu().numpy()
+    fin = np.isfinite(ref_lse)
+    assert np.array_equal(np.isneginf(got), ~fin) and fin[:-1].all()
+    assert np.abs(got[fin] - ref_lse[fin]).max() < 2e-3
+    assert (out[-1] == 0).all()
+
+
 def test_decode_one_token_context_returns_v0_exactly(gpu):
     lens = [1, 1, 17, 16]  # 17: one token in the second page; 16: full page
     kc, vc, bt, indptr, indices, lpl = _paged(lens, 8, 128, 2)

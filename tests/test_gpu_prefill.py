@@ -80,16 +80,49 @@ def test_prefill_edge_cases(gpu):
     _check(gpu, [0, 20, 6, 0, 9], [12, 5, 0, 17, 40], 32, 8, 34)
 
 
-def test_prefill_nan_past_the_end(gpu):
-    """Tokens of a page past kv_len hold NaN bits; they must not leak."""
-    q, kc, vc, qo, kvi, idx, lpl = _case([37], [37], 32, 8, 35, device=gpu)
+@pytest.mark.parametrize("q_len,kv_len", [(37, 37), (37, 1000), (130, 1000)])
+def test_prefill_nan_past_the_end(gpu, q_len, kv_len):
+    """Tokens of the last page past kv_len hold NaN bits; they must not leak.
+    At kv_len 1000 (16 key tiles, 8 tokens in the last page) the last tile
+    is staged and masked inside the pipelined step, not in the prologue."""
+    q, kc, vc, qo, kvi, idx, lpl = _case([q_len], [kv_len], 32, 8, 35, device=gpu)
     last = int(idx[kvi[1] - 1])
-    kc[last, 37 % 16:] = float("nan")
-    vc[last, 37 % 16:] = float("nan")
-    (out, _), _ = _run(gpu, q, kc, vc, qo, kvi, idx, lpl, 32, 8)
-    ref, _ = orc.paged_prefill(u16(q), u16(kc), u16(vc), qo, kvi, idx, lpl)
+    kc[last, kv_len % 16:] = float("nan")
+    vc[last, kv_len % 16:] = float("nan")
+    (out, lse), _ = _run(gpu, q, kc, vc, qo, kvi, idx, lpl, 32, 8)
+    ref, ref_lse = orc.paged_prefill(u16(q), u16(kc), u16(vc), qo, kvi, idx, lpl)
     assert torch.isfinite(out).all()
     assert_attn_close(out.float().cpu().numpy(), ref)
+    assert np.abs(lse.cpu().numpy() - ref_lse).max() < 2e-3
+
+
+def test_prefill_missing_pages_are_hidden(gpu):
+    """Page ids of -1 and past the cache partway through multi-tile requests
+    (and a run of three missing pages) hide their tokens, also on tiles that
+    would otherwise be interior; the pages' blocks hold NaN bits, which must
+    not leak.  Against the oracle's missing-page semantics; finite output."""
+    q_lens, kv_lens = [100, 64, 30, 7], [700, 500, 300, 40]
+    q, kc, vc, qo, kvi, idx, lpl = _case(q_lens, kv_lens, 32, 8, 42, device=gpu)
+    nb = kc.shape[0]
+    hidden = [int(idx[kvi[0] + 5]), int(idx[kvi[2] + 3]), int(idx[kvi[2] + 4]),
+              int(idx[kvi[2] + 5])]
+    idx = idx.copy()
+    idx[kvi[0] + 5] = -1                 # a tile that would be interior
+    idx[kvi[1] + 20] = nb + 7            # past the cache, near the chunk
+    idx[kvi[2] + 3:kvi[2] + 6] = -1      # three missing pages in a row
+    idx[kvi[3]:kvi[4]] = -1              # every page missing: 0 / -inf
+    for p in hidden:                     # no page reads these blocks now
+        kc[p] = float("nan")
+        vc[p] = float("nan")
+    (out, lse), _ = _run(gpu, q, kc, vc, qo, kvi, idx, lpl, 32, 8)
+    ref, ref_lse = orc.paged_prefill(u16(q), u16(kc), u16(vc), qo, kvi, idx, lpl)
+    assert torch.isfinite(out).all()
+    assert_attn_close(out.float().cpu().numpy(), ref)
+    got_lse = lse.cpu().numpy()
+    fin = np.isfinite(ref_lse)
+    assert np.array_equal(np.isneginf(got_lse), ~fin)
+    assert np.abs(got_lse[fin] - ref_lse[fin]).max() < 2e-3
+    assert (out[qo[3]:qo[4]] == 0).all()
 
 
 def test_prefill_long_continuation(gpu):

@@ -238,3 +238,76 @@ def test_stage_from_host_rejects_bad_buffers(gpu):
     pinned[:] = torch.arange(64, dtype=torch.int32)
     ops.stage_from_host(pinned, dev, 64)
     np.testing.assert_array_equal(dev.cpu().numpy(), np.arange(64))
+
+
+def test_decode_step_setup_entry_point_over_many_workgroups(gpu):
+    """kvc_decode_step_setup through the C ABI with 37 requests (ten
+    workgroups, each applying every block-table write itself), block-table
+    writes that move pages, free a row and point past the table (skipped),
+    padding to 45 slots and a plan range: the device image, block table,
+    lengths, slots and page indices equal the oracle's, and nothing past the
+    written ranges changes."""
+    from gpu_offloading_amd import _lib, ops
+
+    rng = np.random.default_rng(80)
+    ms, width, nblk, b = 50, 12, 700, 37
+    bt0 = rng.integers(0, nblk, size=(ms, width)).astype(np.int32)
+    lens0 = rng.integers(0, width * 16 - 1, size=ms).astype(np.int32)
+    ids = rng.permutation(ms)[:b].astype(np.int32)
+    # block-table writes: a new page for some requests, a freed row, one past the table
+    writes = {}
+    for s in ids[:9]:
+        writes[int(s) * width + int(lens0[s]) // 16] = int(rng.integers(0, nblk))
+    freed = int(np.setdiff1d(np.arange(ms), ids)[0])
+    for j in range(width):
+        writes[freed * width + j] = -1
+    writes[ms * width + 3] = 5                      # outside the table: skipped
+    pos = np.fromiter(writes.keys(), np.int64)
+    val = np.fromiter(writes.values(), np.int32)
+    u = len(pos)
+    plan_ints, cap = 10, 12
+    lens = lens0[ids] + 1
+    nblk_req = (lens + 15) // 16
+    indptr = np.zeros(b + 1, np.int32)
+    np.cumsum(nblk_req, out=indptr[1:])
+    o_ids, o_pos, o_ip = cap, cap + b, cap + 2 * b
+    o_lpl = o_ip + b + 1
+    o_la = o_lpl + b
+    o_bpos = (o_la + ms + 1) // 2 * 2
+    o_bval = o_bpos + 2 * u
+    n = o_bval + u
+    h = torch.zeros(n, dtype=torch.int32, pin_memory=True)
+    hv = h.numpy()
+    hv[:plan_ints] = np.arange(100, 100 + plan_ints)
+    hv[o_ids:o_pos] = ids
+    hv[o_pos:o_ip] = lens0[ids]
+    hv[o_ip:o_lpl] = indptr
+    hv[o_lpl:o_la] = np.where(lens % 16 == 0, 16, lens % 16)
+    after = lens0.copy()
+    after[ids] += 1
+    hv[o_la:o_la + ms] = after
+    hv[o_bpos:o_bpos + 2 * u].view(np.int64)[:] = pos
+    hv[o_bval:o_bval + u] = val
+    dev = torch.full((n + 8,), -7, dtype=torch.int32, device=gpu)
+    bt = torch.from_numpy(bt0).to(gpu)
+    seq_lens = torch.from_numpy(lens0).to(gpu)
+    slots = torch.full((45,), 99, dtype=torch.int64, device=gpu)
+    indices = torch.full((int(indptr[-1]) + 5,), -9, dtype=torch.int32, device=gpu)
+    lay = _lib.KvcDecodeStepLayout(plan_ints, cap, n, o_ids, o_pos, o_ip, o_la, o_bpos, o_bval,
+                                   b, u, ms, 16)
+    ops.decode_step_setup(h, dev, lay, bt, seq_lens, slots, indices)
+    torch.cuda.synchronize()
+    exp_bt = bt0.copy()
+    for p, v in writes.items():
+        if p < ms * width:
+            exp_bt[p // width, p % width] = v
+    assert np.array_equal(bt.cpu().numpy(), exp_bt)
+    assert np.array_equal(seq_lens.cpu().numpy(), after)
+    exp_slots, _ = orc.step_slot_mapping(exp_bt, ids, [1] * b, lens0, 45)
+    assert np.array_equal(slots.cpu().numpy(), exp_slots)
+    exp_idx = orc.page_indices(exp_bt, ids, indptr)
+    got_idx = indices.cpu().numpy()
+    assert np.array_equal(got_idx[:len(exp_idx)], exp_idx) and (got_idx[len(exp_idx):] == -9).all()
+    d = dev.cpu().numpy()
+    assert np.array_equal(d[:plan_ints], hv[:plan_ints]) and (d[plan_ints:cap] == -7).all()
+    assert np.array_equal(d[cap:n], hv[cap:n]) and (d[n:] == -7).all()

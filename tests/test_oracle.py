@@ -372,6 +372,62 @@ def test_paged_prefill_one_token_chunks_equal_decode():
     assert np.abs(out - dec).max() < 1e-5 and np.abs(lse - dlse).max() < 1e-5
 
 
+def test_missing_pages_are_hidden():
+    """A page id outside [0, num_blocks) (-1, or past the cache) hides its
+    tokens: decode and prefill equal torch SDPA over the same keys with those
+    tokens masked out by an explicit boolean mask (causal and lower-right for
+    prefill); a request whose pages are all missing gives 0 / -inf.  A planted
+    mistake -- numpy's wrap-around of -1 to the last block, unmasked -- is
+    caught."""
+    from torch.nn.attention.bias import causal_lower_right
+
+    rng = np.random.default_rng(26)
+    nb, hq, hkv, d = 96, 8, 2, 32
+    kv_lens, q_lens = [100, 70, 40], [30, 5, 40]
+    q, kc, vc, qo, kvi, idx, lpl, bt = _prefill_case(rng, q_lens, kv_lens, hq, hkv, d, nb)
+    bad = idx.copy()
+    bad[kvi[0] + 2] = -1            # request 0: page 2 unallocated
+    bad[kvi[1] + 4] = nb + 5        # request 1: its last page past the cache
+    bad[kvi[2]:kvi[3]] = -1         # request 2: every page missing
+    Kf, Vf = torch.from_numpy(orc.bf16_to_f32(kc)), torch.from_numpy(orc.bf16_to_f32(vc))
+    qf = torch.from_numpy(orc.bf16_to_f32(q))
+
+    def masked_sdpa(b, rows, causal):
+        ln = kv_lens[b]
+        pages = bad[kvi[b]:kvi[b + 1]].astype(np.int64)
+        ok = (pages >= 0) & (pages < nb)
+        present = torch.from_numpy(np.repeat(ok, 16)[:ln])
+        safe = torch.from_numpy(np.where(ok, pages, 0))
+        Kb = Kf[safe].flatten(0, 1)[:ln].transpose(0, 1).contiguous()
+        Vb = Vf[safe].flatten(0, 1)[:ln].transpose(0, 1).contiguous()
+        qb = rows.transpose(0, 1).contiguous()                       # [Hq, m, D]
+        mask = present[None, :].expand(qb.shape[1], ln)
+        if causal:
+            mask = mask & causal_lower_right(qb.shape[1], ln)._materialize()
+        o = torch.nn.functional.scaled_dot_product_attention(
+            qb[None], Kb[None], Vb[None], attn_mask=mask, enable_gqa=True)
+        return o[0].transpose(0, 1).numpy()
+
+    out, lse = orc.paged_prefill(q, kc, vc, qo, kvi, bad, lpl, causal=True)
+    for b in (0, 1):
+        ref = masked_sdpa(b, qf[qo[b]:qo[b + 1]], causal=True)
+        assert np.abs(out[qo[b]:qo[b + 1]] - ref).max() < 3e-5
+    assert (out[qo[2]:qo[3]] == 0).all() and np.isneginf(lse[qo[2]:qo[3]]).all()
+    # decode: the last query row of each request, over the whole cache
+    dq = np.stack([q[qo[b + 1] - 1] for b in range(3)])
+    dout, dlse = orc.paged_decode(dq, kc, vc, kvi, bad, lpl)
+    for b in (0, 1):
+        ref = masked_sdpa(b, qf[qo[b + 1] - 1:qo[b + 1]], causal=False)[0]
+        assert np.abs(dout[b] - ref).max() < 3e-5
+    assert (dout[2] == 0).all() and np.isneginf(dlse[2]).all()
+    # the planted mistake: index with the raw ids (-1 wraps to block nb-1)
+    K = orc.bf16_to_f32(kc)[bad[kvi[0]:kvi[1]]].reshape(-1, hkv, d)[:kv_lens[0]]
+    V = orc.bf16_to_f32(vc)[bad[kvi[0]:kvi[1]]].reshape(-1, hkv, d)[:kv_lens[0]]
+    s = K[:, 0] @ orc.bf16_to_f32(dq)[0, 0] / np.sqrt(d)
+    p = np.exp(s - s.max())
+    assert np.abs(p @ V[:, 0] / p.sum() - dout[0, 0]).max() > 1e-3
+
+
 def test_paged_prefill_edge_cases():
     rng = np.random.default_rng(23)
     q, kc, vc, qo, kvi, idx, lpl, bt = _prefill_case(rng, [3, 0, 4], [2, 5, 4], 4, 2, 16)

@@ -3,7 +3,9 @@ partials live in the library's own device array) through the C ABI: on two
 calls in a row, the second with a smaller batch, its output and lse equal
 those of kvc_batch_decode_run with a caller workspace bit for bit (the same
 kernels on the same partial layout), and match the oracle within max 2e-2 /
-mean 2e-3.  A batch whose partials exceed the array is refused."""
+mean 2e-3.  A batch whose partials exceed the array is refused.  The call
+is captured in a HIP graph (its first call on the device inside the capture)
+and replayed, and an eager call leaves the device's free memory unchanged."""
 import ctypes
 
 import numpy as np
@@ -67,6 +69,64 @@ def _run_both(gpu, lens, seed, segs=None):
     assert_attn_close(out_na.float().cpu().numpy(), ref)
     assert np.abs(lse_na.cpu().numpy() - ref_lse).max() < 2e-3
     return sched
+
+
+def test_noalloc_decode_captured_in_a_graph_matches_eager(gpu):
+    """What the entry point is for: a caller that cannot allocate captures it
+    in a HIP graph.  Only a workspace run (which loads the kernels) precedes
+    the capture, so the first allocation-free call on this device -- the
+    lookup of its array's address -- happens inside the capture.  Three
+    replays with new q (eager work and synchronisations between them) each
+    equal the eager workspace run bit for bit; an eager call then leaves the
+    device's free memory unchanged (hipMemGetInfo)."""
+    print("noalloc: capture of the first call on the device", flush=True)
+    lens = [3000, 17, 1, 900, 4096, 256, 33]
+    kc, vc, q, w, _ = _batch(gpu, lens, 60, segs=97)
+    assert w._sched.max_partitions > 1
+    lib = _lib.load()
+    B = len(lens)
+    ws = w._workspace
+    q_in = torch.zeros_like(q)
+    out_g = torch.empty(B, 32, 128, dtype=torch.bfloat16, device=gpu)
+    lse_g = torch.empty(B, 32, dtype=torch.float32, device=gpu)
+    out_ws, lse_ws = torch.empty_like(out_g), torch.empty_like(lse_g)
+
+    def workspace_run(qq, stream):
+        st = lib.kvc_batch_decode_run(*_args(w, qq, kc, vc), ws.data_ptr(), ws.numel(),
+                                      out_ws.data_ptr(), out_ws.stride(0), lse_ws.data_ptr(),
+                                      stream)
+        assert st == 0, lib.kvc_last_error()
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        workspace_run(q_in, side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = lib.kvc_batch_decode_run_noalloc(*_args(w, q_in, kc, vc), out_g.data_ptr(),
+                                              out_g.stride(0), lse_g.data_ptr(),
+                                              torch.cuda.current_stream().cuda_stream)
+    assert st == 0, lib.kvc_last_error()
+    g = torch.Generator(device=gpu).manual_seed(61)
+    for rep in range(3):
+        q_new = torch.randn(q.shape, generator=g, device=gpu).to(torch.bfloat16)
+        q_in.copy_(q_new)
+        graph.replay()
+        got, got_lse = out_g.clone(), lse_g.clone()
+        torch.cuda.synchronize()
+        workspace_run(q_new, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert torch.equal(got, out_ws) and torch.equal(got_lse, lse_ws), rep
+    free0 = torch.cuda.mem_get_info()[0]
+    st = lib.kvc_batch_decode_run_noalloc(*_args(w, q_in, kc, vc), out_g.data_ptr(),
+                                          out_g.stride(0), lse_g.data_ptr(),
+                                          torch.cuda.current_stream().cuda_stream)
+    assert st == 0, lib.kvc_last_error()
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    del graph
 
 
 def test_noalloc_decode_matches_the_workspace_run_twice(gpu):
