@@ -282,13 +282,19 @@ class PagedKVCache:
 
     @property
     def pages_free(self) -> int:
+        """Pages an allocation can take: the free list plus the pages of
+        swap-outs still copying (``alloc_pages`` waits for those copies when
+        it needs their pages).  So a scheduler sees a swapped-out victim's
+        pages as freed at once, as after the reference's ``free_seq``
+        (scheduler.py:329-333)."""
         self._require_dynamic()
-        return self._pool.pages_free
+        return self._pool.pages_free + self._swaps.pending_pages
 
     @property
     def pages_in_use(self) -> int:
+        """Pages owned by sequences (``total_pages - pages_free``)."""
         self._require_dynamic()
-        return self._pool.pages_in_use
+        return self._pool.pages_in_use - self._swaps.pending_pages
 
     def seq_pages(self, seq_id: int) -> int:
         if not self._dynamic_pages:

@@ -39,6 +39,13 @@ class SwapLedger:
         # sequence -> event of its restore still in flight
         self.pending_in: dict[int, Any] = {}
 
+    @property
+    def pending_pages(self) -> int:
+        """Pages detached by swap-outs whose copies may still run: they are
+        not owned by any sequence, and an allocation that needs them gets
+        them (``reclaim`` waits for their copy)."""
+        return sum(len(pages) for _, pages, _ in self.pending_free)
+
     def add_swap_out(self, event, pages: Sequence[int], keepalive: Iterable = ()) -> None:
         """``pages`` were detached by a swap-out whose copies end at ``event``."""
         self.pending_free.append((event, list(pages), list(keepalive)))

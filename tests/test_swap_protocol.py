@@ -140,8 +140,13 @@ def test_paged_kv_cache_follows_the_protocol(monkeypatch):
     cache.alloc_pages(0, 6)
     ev = FakeEvent("out0")
     _swap_out(cache._swaps, cache._pool, 0, ev)     # the bookkeeping swap_out does
+    # the victim's pages count as free for the scheduler at once (an
+    # allocation that needs them waits for the copy), as after free_seq
+    assert cache.pages_free == 8 and cache.pages_in_use == 0
+    assert cache._swaps.pending_pages == 6
     cache.alloc_pages(1, 2)                          # served by the free pages
     assert ev.synchronized == 0
+    assert cache.pages_free == 6 and cache.pages_in_use == 2
     cache.alloc_pages(2, 3)                          # needs the swapped-out pages
     assert ev.synchronized == 1 and cache.seq_pages(2) == 3
     cur = FakeStream()
