@@ -8,7 +8,7 @@
 // Work item = (request, tile of kTileRows query rows) x one KV head.  A query
 // row is a (token, query head) pair: the `group` query heads that share a KV
 // head are packed into the rows of one tile, so every K/V tile staged in LDS
-// serves all of them (GQA reuse).  The four waves of a workgroup own 32 rows
+// serves all of them (GQA reuse).  The eight waves of a workgroup own 32 rows
 // each; the workgroup walks the request's keys in tiles of 64.
 //
 // Per key tile, per wave, with v_mfma_f32_32x32x16_bf16 (A: lane l = row l%32,
@@ -32,11 +32,10 @@
 // buffer_load_dwordx4 ... lds) as unpadded [key][dim] rows whose 16-byte
 // chunks are XOR-swizzled by key, so that the MFMA operand reads hit distinct
 // banks: K as 16-byte reads of one key's dims, V^T through the transposing
-// ds_read_b64_tr_b16.  Two LDS buffers per operand, K staged two tiles ahead
-// and V one, one barrier per tile.  V rows past the end of the cache or in a
-// missing page load as zeros (the buffer load is bounded to the page's valid
-// tokens), so a masked key contributes exactly 0 even if the page holds NaN
-// bits.
+// ds_read_b64_tr_b16.  Two LDS buffers per operand.  V rows past the end of
+// the cache or in a missing page load as zeros (the buffer load is bounded to
+// the page's valid tokens), so a masked key contributes exactly 0 even if the
+// page holds NaN bits.
 #include "kvc_common.h"
 
 #include <algorithm>
@@ -54,9 +53,9 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kWaveRows = 32;                 // query rows per wave
-constexpr int kTileRows = 4 * kWaveRows;      // query rows per workgroup
+constexpr int kTileRows = 8 * kWaveRows;      // query rows per workgroup
 constexpr int kKeys = 64;                     // keys per tile
 constexpr int kPage = 16;
 constexpr int kD = 128;
@@ -112,19 +111,35 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Two waves per SIMD (<= 256 VGPRs, no AGPRs).  The softmax's VALU work per
-// key tile is about as long as the tile's 32 MFMAs, so each wave runs them
-// side by side: step j computes the softmax of tile j while the MFMAs of the
-// scores of tile j+1 run, then P_j V_j while the next tiles are staged.  The
-// softmax is kept lean: per-key tests only on boundary tiles, once per score
-// (hidden scores set to -inf while the row max is taken), the scale folded
+// Eight waves in two teams of four, one workgroup per CU, two waves per SIMD
+// (<= 256 VGPRs, no AGPRs): wave w of team 0 and wave w of team 1 share SIMD
+// w.  Each team owns 128 query rows and both teams read the same K/V tiles.
+// Per 64-key tile a wave has two phases of about equal length: an MFMA phase
+// (the 16 MFMAs of O^T += V^T P^T for the previous tile, then the 16 of
+// S^T = K Q^T for this tile, LDS operands read ahead, no other work) and a
+// VALU phase (the tile's row max, the lazy O rescale, the exponentials, P
+// packed to bf16 and summed).  Team 1 runs one phase behind team 0 and every
+// phase ends on a workgroup barrier, so on each SIMD one wave's MFMA chain
+// runs while the other wave does its softmax: the matrix pipe does not wait
+// for the VALU, and the VALU is never starved by the matrix pipe.  The MFMA
+// team raises its priority for its phase.
+//
+// Slots 2j and 2j+1 each end on a workgroup barrier.  M_j: O += P_{j-1}
+// V_{j-1} (j >= 1) and S_j = K_j Q (j < ntiles); X_j: softmax of S_j into
+// P_j.  Team 0 runs M_j in slot 2j and X_j in slot 2j+1; team 1 runs X_{j-1}
+// in slot 2j and M_j in slot 2j+1.  Team 1 also stages: at the start of
+// slot 2j each of its waves issues the direct-to-LDS loads of its page
+// (w - 4) of K_{j+1} and of V_j (the buffers they overwrite were last read
+// in slot 2j-1), from page offsets resolved two tiles earlier, and waits
+// for them before the barrier that ends slot 2j+1; page resolution and the
+// next page-id fetch come after its softmax, off the MFMA team's path.  The
+// softmax is lean: per-key tests only on boundary tiles, the scale folded
 // into one FMA per score, the O rescale skipped unless a row max grows by
 // more than 2^8, P packed to bf16 with v_cvt_pk_bf16_f32 and summed from the
-// packed pairs with v_dot2_f32_bf16, the row max exchanged between the two
-// lane halves with v_permlane32_swap, and the row sum kept per lane half
-// until the end.
+// packed pairs with v_dot2_f32_bf16, the row max exchanged between the lane
+// halves with v_permlane32_swap.
 template <int G>
-__global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int kTokPerWave = kWaveRows / G;
   __shared__ KTile ktiles[2];
   __shared__ VTile vtiles[2];
@@ -136,6 +151,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   const int q_off = it1.x, page_off = it1.y, ntiles = it1.z, npages = it1.w;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
+  const int team = wave >> 2;
+  const int pw_idx = wave & 3;        // the page of a tile this wave stages (team 1)
   const int lane = threadIdx.x & 63;
   const int r = lane & 31;
   const int half = lane >> 5;
@@ -164,15 +181,15 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   const char* kbase = reinterpret_cast<const char*>(a.k_cache);
   const char* vbase = reinterpret_cast<const char*>(a.v_cache);
   const int64_t tok_bytes = a.token_stride * 2;
-  // K (direct to LDS): wave w loads page w of a tile; its load i fetches
-  // keys 4i .. 4i+3 of the page, lane L key 4i + L/16, the chunk whose
-  // swizzled slot is L%16.  V the same way, with its own swizzle.
-  uint32_t k_lane_off[4], v_lane_off[4];
+  // Direct-to-LDS staging: this wave's load i fetches keys 4i .. 4i+3 of its
+  // page, lane L key 4i + L/16, the chunk whose swizzled slot is L%16 (K and
+  // V each with their own swizzle).
+  uint32_t lane_k[4], lane_v[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int key = 4 * i + (lane >> 4);
-    k_lane_off[i] = uint32_t(key * tok_bytes + (head_off + ((lane & 15) ^ (key & 15)) * 8) * 2);
-    v_lane_off[i] = uint32_t(key * tok_bytes + (head_off + ((lane & 15) ^ (4 * (key & 3))) * 8) * 2);
+    lane_k[i] = uint32_t(key * tok_bytes + (head_off + ((lane & 15) ^ (key & 15)) * 8) * 2);
+    lane_v[i] = uint32_t(key * tok_bytes + (head_off + ((lane & 15) ^ (4 * (key & 3))) * 8) * 2);
   }
   // Every global_load_lds of this wave has written LDS (vmcnt 0).
   auto wait_dma = []() __attribute__((always_inline)) { __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); };
@@ -187,48 +204,41 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   auto fetch_ids = [&](int tile) __attribute__((always_inline)) {
     return RawIds{a.indices[min(page_off + tile * 4 + (lane & 3), last_index)]};
   };
-  // Wave-uniform byte offsets of a tile's four blocks (the host keeps a block
-  // stride under 4 GiB), computed once and used for K in one step and for V
-  // in the next; bit u of `ok` says page u is real (inside the request and
-  // the cache), the others read block 0 and are masked.  (Plain scalars, not
-  // an array: a copy carried across steps must stay in registers.)
+  // Byte offset of this wave's page of a tile (the host keeps a block stride
+  // under 4 GiB) and the tile's present pages: bit u of `ok` says page u is
+  // real (inside the request and the cache); the others read block 0 and
+  // are masked.  Pages [0, pages_here) of the item exist in the request and
+  // the index array; a present page also needs an id in [0, num_blocks).  The
+  // four tests run on lanes 0..3 at once and one ballot collects them.
   const uint32_t blk32 = uint32_t(a.block_stride * 2);
-  struct Pages { uint64_t off; int ok; };  // off: this wave's page (page `wave`)
-  // Pages [0, pages_here) of the item exist in the request and the index
-  // array; a present page also needs an id in [0, num_blocks).  The four
-  // tests run on lanes 0..3 at once and one ballot collects them.
+  struct Pages { uint64_t off; int ok; };
   const int pages_here = min(npages, last_index - page_off + 1);
   auto resolve = [&](const RawIds& t, int tile) __attribute__((always_inline)) {
     const bool good = (tile * 4 + (lane & 3) < pages_here) & (uint32_t(t.v) < uint32_t(num_blocks32));
     const int ok = int(__builtin_amdgcn_ballot_w64(good) & 0xF);
     const int32_t v = good ? t.v : 0;
-    return Pages{uint64_t(uint32_t(__builtin_amdgcn_readlane(v, wave))) * blk32, ok};
+    return Pages{uint64_t(uint32_t(__builtin_amdgcn_readlane(v, pw_idx))) * blk32, ok};
   };
   // Direct loads from memory into LDS (global_load_lds_dwordx4 and
   // buffer_load_dwordx4 ... lds, one 16-byte chunk per lane, lane L at LDS
   // offset 16L from the wave-uniform address in M0).  They are issued as
   // inline assembly so that the compiler does not make every later LDS read
   // wait for them (it cannot tell the buffer being filled from the one being
-  // read); the step waits for them itself (vmcnt 0) before the barrier that
+  // read); each wave waits for its own (vmcnt 0) before the barrier that
   // publishes the tiles.  No compiler-generated code here uses M0 (M0 is a
   // reserved register hipcc will not take as a clobber;
   // tests/test_prefill_m0.py checks the built assembly for any other use).
   auto lds_addr = [](const void* p) __attribute__((always_inline)) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t*)p));
   };
-
-  // K goes straight from memory into LDS (global_load_lds_dwordx4): one
-  // instruction of a wave fills 1 KB of LDS, lane L's 16 bytes at offset
-  // 16L, so load i of wave w fills keys 4i .. 4i+3 of page w (tile rows
-  // 16w + 4i ..), lane L fetching the chunk that belongs in slot L%16 of key
-  // 4i + L/16: one block address per wave and tile.  The loads are waited
-  // for (vmcnt) before the barrier that publishes the tile.
+  // K: one instruction of a wave fills 1 KB of LDS (keys 4i .. 4i+3 of the
+  // wave's page): one block address per wave and tile.
   auto dma_k = [&](KTile& buf, const Pages& p) __attribute__((always_inline)) {
     const char* blk = kbase + p.off;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-                   :: "s"(lds_addr(buf.b + (wave * kPage + 4 * i) * kKRow)), "v"(k_lane_off[i]),
+                   :: "s"(lds_addr(buf.b + (pw_idx * kPage + 4 * i) * kKRow)), "v"(lane_k[i]),
                       "s"(blk) : "memory");
   };
   // V goes into LDS the same way, through a buffer load bounded to the
@@ -237,7 +247,14 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   // no such care: a key's score depends on its own K row only, and tiles
   // holding such keys are processed with the per-key tests, which never
   // read its score.
-  auto dma_v_page = [&](VTile& buf, const Pages& p, int bytes) __attribute__((always_inline)) {
+  const int page_bytes = kPage * int(tok_bytes);  // under 2 GiB (host check)
+  auto dma_v = [&](VTile& buf, const Pages& p, int tile) __attribute__((always_inline)) {
+    const bool real = (p.ok >> pw_idx) & 1;
+    int bytes = real ? page_bytes : 0;
+    if ((tile + 1) * kKeys > kv_len) {
+      const int rem = max(0, min(kPage, kv_len - tile * kKeys - pw_idx * kPage));
+      bytes = real ? rem * int(tok_bytes) : 0;
+    }
     const uint64_t blk = reinterpret_cast<uint64_t>(vbase + p.off);
     const i32x4_t rsrc = {__builtin_amdgcn_readfirstlane(int(uint32_t(blk))),
                           __builtin_amdgcn_readfirstlane(int(uint32_t(blk >> 32) & 0xFFFF)),
@@ -245,38 +262,23 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                   :: "s"(lds_addr(buf.b + (wave * kPage + 4 * i) * kKRow)), "v"(v_lane_off[i]),
+                   :: "s"(lds_addr(buf.b + (pw_idx * kPage + 4 * i) * kKRow)), "v"(lane_v[i]),
                       "s"(rsrc) : "memory");
   };
-  // Bytes of each page's valid tokens: all 16 on a tile inside the cache
-  // (every tile but a request's last), fewer in the page holding kv_len,
-  // none in a missing page.
-  const int page_bytes = kPage * int(tok_bytes);  // under 2 GiB (host check)
-  auto dma_v = [&](VTile& buf, const Pages& p, int tile) __attribute__((always_inline)) {
-    const bool real = (p.ok >> wave) & 1;
-    if ((tile + 1) * kKeys <= kv_len) {
-      dma_v_page(buf, p, real ? page_bytes : 0);
-    } else {
-      const int rem = max(0, min(kPage, kv_len - tile * kKeys - wave * kPage));
-      dma_v_page(buf, p, real ? rem * int(tok_bytes) : 0);
-    }
-  };
 
-  // The first tiles' page ids are fetched now, beside the Q loads.
-  const RawIds raw0 = fetch_ids(0);
-  RawIds raw1{};
-  if (ntiles > 1) raw1 = fetch_ids(1);
   // V tiles start as zeros: should a bounded load leave the LDS rows of
   // out-of-range lanes untouched, they hold zeros or earlier valid rows,
-  // never stale bits from before the kernel.  Each wave clears the rows its
-  // own loads fill (rows 16*wave .. +15 of both buffers) and waits for that
-  // before issuing them.
+  // never stale bits from before the kernel.  Each V-staging wave clears the
+  // rows its own loads fill (rows 16*(w-4) .. +15 of both buffers) and waits
+  // for that before issuing them.
+  if (team == 1) {
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    uint8_t* row = vtiles[c >> 2].b + (wave * kPage + 4 * (c & 3) + (lane >> 4)) * kKRow;
-    *reinterpret_cast<uint4*>(row + (lane & 15) * 16) = make_uint4(0, 0, 0, 0);
+    for (int c = 0; c < 8; ++c) {
+      uint8_t* row = vtiles[c >> 2].b + (pw_idx * kPage + 4 * (c & 3) + (lane >> 4)) * kKRow;
+      *reinterpret_cast<uint4*>(row + (lane & 15) * 16) = make_uint4(0, 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkmcnt0);
   }
-  __builtin_amdgcn_s_waitcnt(kWaitLgkmcnt0);
 
   uint32_t v_rd[4];
   {
@@ -312,6 +314,16 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[db][e] = 0.f;
+  f32x16_t s[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
+  uint32_t pw[2][8];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pw[kb][e] = 0u;
   // m_run: the row's running max (base 2, scaled); l_half: the running sum
   // of p over this lane's half of every tile's keys (lane l^32 holds the
   // other half), both under the same m_run.
@@ -321,167 +333,22 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
   // Accumulator entry e of key block kb holds key 32kb + 8(e/4) + 4half + e%4
   // of the tile, which lies in page 2kb + e/8 of the tile.  Interior tiles
   // (every key visible to every row of the workgroup, all pages present)
-  // skip the per-key tests: masked = false.  rel = the key offset (within
-  // the lane's half of the tile) the row may still see.
-  auto visible = [&](int rel, int ok, int kb, int e, auto masked) __attribute__((always_inline)) {
-    if constexpr (decltype(masked)::value)
-      return (32 * kb + 8 * (e >> 2) + (e & 3)) <= rel && ((ok >> (2 * kb + (e >> 3))) & 1);
-    else
-      return true;
+  // skip the per-key tests.  rel = the key offset (within the lane's half of
+  // the tile) the row may still see.
+  auto visible = [&](int rel, int ok, int kb, int e) __attribute__((always_inline)) {
+    return (32 * kb + 8 * (e >> 2) + (e & 3)) <= rel && ((ok >> (2 * kb + (e >> 3))) & 1);
   };
-  auto rel_of = [&](int tile) __attribute__((always_inline)) {
-    return limit - tile * kKeys - 4 * half;
-  };
-  // Max of the raw scores of quarter q (key block q/2, entries 8(q%2) .. +7).
-  // On a tile that needs the per-key tests, the scores of keys the row may
-  // not see become -inf here, in place: the exponentials then need no tests
-  // (exp2(-inf) = 0, the scale being positive and finite).
-  auto quarter_max = [&](f32x16_t (&s)[2], int q, int rel, int ok, float mx, auto masked)
-      __attribute__((always_inline)) {
-#pragma unroll
-    for (int e = 8 * (q & 1); e < 8 * (q & 1) + 8; ++e) {
-      if constexpr (decltype(masked)::value)
-        s[q >> 1][e] = visible(rel, ok, q >> 1, e, masked) ? s[q >> 1][e] : -INFINITY;
-      mx = fmaxf(mx, s[q >> 1][e]);
-    }
-    return mx;
-  };
-  // The same with the tile's two key blocks held in separate arrays.
-  auto quarter_max2 = [&](f32x16_t& s0, f32x16_t& s1, int q, int rel, int ok,
-                          float mx, auto masked) __attribute__((always_inline)) {
-    f32x16_t& s = (q >> 1) ? s1 : s0;
-#pragma unroll
-    for (int e = 8 * (q & 1); e < 8 * (q & 1) + 8; ++e) {
-      if constexpr (decltype(masked)::value)
-        s[e] = visible(rel, ok, q >> 1, e, masked) ? s[e] : -INFINITY;
-      mx = fmaxf(mx, s[e]);
-    }
-    return mx;
-  };
-  // Folds a tile's row max (this lane's 32 keys and lane l^32's; the raw
-  // scores, as the scale is positive) into the running max.  A row's running
-  // max only moves when its max grew by more than kRescaleLog2 (base-2
-  // units); otherwise the stale max stays, p <= 2^8, and the rescale of O and
-  // l is skipped -- same result, 65 fewer multiplies.
-  auto fold_max = [&](float mx) __attribute__((always_inline)) {
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
-                                                     false, false);
-    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-    // Each row decides for itself (the branch is only skipped when no row of
-    // the wave needs it), so a row's result does not depend on which other
-    // rows share its wave.
-    const float cand = fmaxf(m_run, mx * a.scale_log2);
-    const bool grow = cand > m_run + kRescaleLog2;
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-      const float alpha = grow ? fast_exp2(m_run - cand) : 1.f;
-      m_run = grow ? cand : m_run;
-      l_half *= alpha;
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
-    }
-  };
-  // Exponent pair i (0..15) of a tile: p = exp2(S scale - m_run) for entries
-  // 2(i%8), +1 of key block i/8, packed to a bf16 pair in S^T accumulator
-  // order and added (as rounded) into `sum`.
-  auto exp_pair = [&](const f32x16_t (&s)[2], int i, uint32_t (&pw)[2][8], float& sum)
-      __attribute__((always_inline)) {
-    const int kb = i >> 3, e = 2 * (i & 7);
-    const float p0 = fast_exp2(fmaf(s[kb][e], a.scale_log2, -m_run));
-    const float p1 = fast_exp2(fmaf(s[kb][e + 1], a.scale_log2, -m_run));
-    pw[kb][e >> 1] = pack_bf16(p0, p1);
-    sum = dot2_bf16(pw[kb][e >> 1], ones, sum);
-  };
-  // The 16 score MFMAs of a tile, alone (first tile).
-  auto scores = [&](const KTile& buf, f32x16_t (&s)[2]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      s[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_operand(buf, i), qb[i >> 1], s[i & 1],
-                                                         0, 0, 0);
-  };
-
   // Tiles [0, n_full) are interior for every row of the workgroup when all
   // their pages are present: all its rows see keys up to at least lim_lo
   // (its first token's limit).
   const int lim_lo = a.causal ? tok0 + kv_len - q_len : kv_len - 1;
   const int n_full = max(0, min(ntiles, (lim_lo + 1) / kKeys));
 
-  // Step j.  On entry: s_cur = raw S^T of tile j, already folded into
-  // m_run; K of tile j+1 in ktiles[(j+1)&1] and V of tile j in vtiles[j&1];
-  // pages_v = pages of tile j+1; raw_k = page ids of tile j+2 (in flight).
-  // The step first issues the direct-to-LDS loads of K of tile j+2 (into the
-  // K buffer tile j used) and V of tile j+1.  A wave issues in order and an
-  // MFMA occupies the matrix pipe for 32 cycles, so the step then
-  // interleaves, in program order (fenced with sched_barrier):
-  //   1. the 16 score MFMAs of tile j+1 with the exponentials of tile j,
-  //      one exponent pair per MFMA: key block 1's MFMAs first (into s_b1)
-  //      beside block 0's exponentials, then block 0's, straight into
-  //      s_cur[0], which those have finished reading;
-  //   2. the 16 MFMAs of O^T += V^T P^T for tile j with the row max of tile
-  //      j+1;
-  // each with its LDS operand read three MFMAs ahead; then it folds the row
-  // max into m_run, moves s_b1 into s_cur[1], waits for its loads and ends
-  // on the barrier.  mn: whether tile j+1 needs the per-key tests (its row
-  // max then also sets the scores of hidden keys to -inf, so tile j's
-  // exponentials, one step later, run without tests).
-  f32x16_t s_cur[2];
-  int ok_cur = 0;
-  Pages pages_v{0, 0};
-  RawIds raw_k{};
-  auto step = [&](int j, auto mn, auto has_next) __attribute__((always_inline)) {
-    constexpr bool kNext = decltype(has_next)::value;
-    // The ids of tile j+2 (loaded last step) are read before this step
-    // issues any load.
-    const bool k2 = j + 2 < ntiles;
-    const Pages pages_k = resolve(raw_k, j + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    if (k2) dma_k(ktiles[j & 1], pages_k);
-    if constexpr (kNext) dma_v(vtiles[(j + 1) & 1], pages_v, j + 1);
-    if (j + 3 < ntiles) raw_k = fetch_ids(j + 3);
-
-    // 1. scores of tile j+1 beside the exponentials of tile j.
-    uint32_t pw[2][8];
-    f32x16_t s_b1;  // tile j+1's scores, key block 1
-    {
-      float sum0 = 0.f, sum1 = 0.f;
-      if constexpr (kNext) {
-        const KTile& kb = ktiles[(j + 1) & 1];
-        // MFMA i computes k-step mi(i) / 2 of key block mi(i) % 2: block 1
-        // for i < 8, block 0 after; each block's k-steps stay in order.
-        auto mi = [](int i) { return i < 8 ? 2 * i + 1 : 2 * (i - 8); };
-        const f32x16_t zero = {};
-        bf16x8_t kop[16];
-#pragma unroll
-        for (int i = 0; i < 3; ++i) kop[i] = k_operand(kb, mi(i));
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          if (i + 3 < 16) kop[i + 3] = k_operand(kb, mi(i + 3));
-          if (i < 8)
-            s_b1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[i], qb[mi(i) >> 1],
-                                                          i == 0 ? zero : s_b1, 0, 0, 0);
-          else
-            s_cur[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[i], qb[mi(i) >> 1],
-                                                              i == 8 ? zero : s_cur[0], 0, 0, 0);
-          exp_pair(s_cur, i, pw, (i & 1) ? sum1 : sum0);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) exp_pair(s_cur, i, pw, (i & 1) ? sum1 : sum0);
-      }
-      l_half += sum0 + sum1;
-    }
-
-    // 2. P_j V_j beside the row max of tile j+1.
-    {
-      const VTile& vb = vtiles[j & 1];
-      const int rel = rel_of(j + 1);
-      float mx = kNegBig;
+  // M_j: O += P_{j-1} V_{j-1} (do_o), then S_j = K_j Q (do_s), each MFMA's
+  // LDS operand read four MFMAs ahead.
+  auto mfma_phase = [&](int j, auto do_o_c, auto do_s_c) __attribute__((always_inline)) {
+    if constexpr (decltype(do_o_c)::value) {
+      const VTile& vb = vtiles[(j - 1) & 1];
       bf16x8_t vop[16];
 #pragma unroll
       for (int i = 0; i < 3; ++i) vop[i] = v_operand(vb, i);
@@ -492,53 +359,163 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(PrefillArgs a
         const uint32_t* pp = &pw[st >> 1][4 * (st & 1)];
         const bf16x8_t pb = as_bf16x8(make_uint4(pp[0], pp[1], pp[2], pp[3]));
         o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[i], pb, o[i & 3], 0, 0, 0);
-        if constexpr (kNext) {
-          // key block 1 first: block 0's last MFMA has just been issued
-          if (i < 4) mx = quarter_max2(s_cur[0], s_b1, i ^ 2, rel, pages_v.ok, mx, mn);
-        }
         __builtin_amdgcn_sched_barrier(0);
       }
-      if constexpr (kNext) fold_max(mx);
     }
-    wait_dma();
-    __syncthreads();
-    if constexpr (kNext) {
-      s_cur[1] = s_b1;
-      ok_cur = pages_v.ok;
-      pages_v = pages_k;
+    if constexpr (decltype(do_s_c)::value) {
+      const KTile& kb = ktiles[j & 1];
+      const f32x16_t zero = {};
+      bf16x8_t kop[16];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) kop[i] = k_operand(kb, i);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (i + 3 < 16) kop[i + 3] = k_operand(kb, i + 3);
+        s[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[i], qb[i >> 1],
+                                                           i < 2 ? zero : s[i & 1], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  // X_j: on a tile that needs the per-key tests (a boundary tile or a
+  // missing page) the scores of keys the row may not see become -inf, in
+  // place (the exponentials then need no tests: exp2(-inf) = 0, the scale
+  // being positive and finite); then the row max of S_j is folded into m_run
+  // with the lazy rescale of O and l, and P_j = exp2(S scale - m_run) is
+  // packed to bf16 in S^T accumulator order and summed into l_half.  The
+  // masking is a block of its own that only rewrites S, so O has one path
+  // through the phase.
+  auto valu_phase = [&](int j, int ok) __attribute__((always_inline)) {
+    if (!(j < n_full && ok == 0xF)) {
+      const int rel = limit - j * kKeys - 4 * half;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[kb][e] = visible(rel, ok, kb, e) ? s[kb][e] : -INFINITY;
+    }
+    float mx = kNegBig;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kb][e]);
+    // Fold the tile's row max (this lane's 32 keys and lane l^32's; the raw
+    // scores, as the scale is positive) into the running max.  A row's
+    // running max only moves when its max grew by more than kRescaleLog2
+    // (base-2 units); otherwise the stale max stays, p <= 2^8, and the
+    // rescale of O and l is skipped.  Each row decides for itself, so a
+    // row's result does not depend on which other rows share its wave.
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                     false, false);
+    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    const float cand = fmaxf(m_run, mx * a.scale_log2);
+    const bool grow = cand > m_run + kRescaleLog2;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float alpha = grow ? fast_exp2(m_run - cand) : 1.f;
+      m_run = grow ? cand : m_run;
+      l_half *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[db] *= alpha;
+    }
+    float sum0 = 0.f, sum1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kb = i >> 3, e = 2 * (i & 7);
+      const float p0 = fast_exp2(fmaf(s[kb][e], a.scale_log2, -m_run));
+      const float p1 = fast_exp2(fmaf(s[kb][e + 1], a.scale_log2, -m_run));
+      pw[kb][e >> 1] = pack_bf16(p0, p1);
+      if (i & 1) sum1 = dot2_bf16(pw[kb][e >> 1], ones, sum1);
+      else sum0 = dot2_bf16(pw[kb][e >> 1], ones, sum0);
+      if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+    }
+    l_half += sum0 + sum1;
+  };
+
+  // Slots 2j and 2j+1 (each ends on a workgroup barrier): team 0 runs M_j
+  // then X_j, team 1 runs X_{j-1} then M_j.  Each team has its own copy of the
+  // code (the team is a compile-time constant in `run`), with the first and
+  // last tiles peeled, so the loop body is straight-line code in which O, S
+  // and P keep their registers; the teams only have to meet the same
+  // barriers, not the same instructions.
+  using yes = std::true_type;
+  using no = std::false_type;
+  auto run = [&](auto team_c) __attribute__((always_inline)) {
+    constexpr int kTeam = decltype(team_c)::value;
+    auto mfma = [&](int j, auto do_o_c, auto do_s_c) __attribute__((always_inline)) {
+      __builtin_amdgcn_s_setprio(1);
+      mfma_phase(j, do_o_c, do_s_c);
+      __builtin_amdgcn_s_setprio(0);
+    };
+    if (kTeam == 0) {
+      // Team 0 stages nothing; it only needs each tile's present pages for
+      // its VALU phase, resolved one tile ahead after that phase.
+      RawIds raw = fetch_ids(0);
+      int ok_cur = resolve(raw, 0).ok;   // tile j's, from slot 2j+1 on
+      raw = fetch_ids(1);
+      __syncthreads();
+      mfma(0, no{}, yes{});
+      __syncthreads();
+      valu_phase(0, ok_cur);
+      ok_cur = resolve(raw, 1).ok;
+      raw = fetch_ids(2);
+      __syncthreads();
+      for (int j = 1; j < ntiles; ++j) {
+        mfma(j, yes{}, yes{});
+        __syncthreads();
+        valu_phase(j, ok_cur);
+        ok_cur = resolve(raw, j + 1).ok;
+        raw = fetch_ids(j + 2);
+        __syncthreads();
+      }
+      mfma(ntiles, yes{}, no{});
+      __syncthreads();
+      __syncthreads();
+    } else {
+      // Team 1 stages K_{j+1} and V_j at the start of slot 2j, from pages
+      // resolved two tiles ahead, and waits for them at the end of slot 2j+1.
+      RawIds raw = fetch_ids(0);
+      Pages pv = resolve(raw, 0);        // tile j's pages, at slot 2j
+      raw = fetch_ids(1);
+      Pages pk = resolve(raw, 1);        // tile j+1's
+      raw = fetch_ids(2);
+      int ok_prev = 0;                   // tile j-1's present pages
+      // After slot 2j's loads are issued: resolve tile j+2, fetch tile j+3's
+      // page ids and shift the window.
+      auto advance = [&](int j) __attribute__((always_inline)) {
+        const Pages pn = resolve(raw, j + 2);
+        raw = fetch_ids(j + 3);
+        ok_prev = pv.ok;
+        pv = pk;
+        pk = pn;
+      };
+      dma_k(ktiles[0], pv);
+      wait_dma();
+      __syncthreads();
+      if (1 < ntiles) dma_k(ktiles[1], pk);
+      dma_v(vtiles[0], pv, 0);
+      advance(0);
+      __syncthreads();
+      mfma(0, no{}, yes{});
+      wait_dma();
+      __syncthreads();
+      for (int j = 1; j < ntiles; ++j) {
+        if (j + 1 < ntiles) dma_k(ktiles[(j + 1) & 1], pk);
+        dma_v(vtiles[j & 1], pv, j);
+        valu_phase(j - 1, ok_prev);
+        advance(j);
+        __syncthreads();
+        mfma(j, yes{}, yes{});
+        wait_dma();
+        __syncthreads();
+      }
+      valu_phase(ntiles - 1, ok_prev);
+      __syncthreads();
+      mfma(ntiles, yes{}, no{});
+      __syncthreads();
     }
   };
   if (ntiles > 0) {
-    const Pages p0 = resolve(raw0, 0);
-    dma_k(ktiles[0], p0);
-    dma_v(vtiles[0], p0, 0);
-    if (ntiles > 1) {
-      pages_v = resolve(raw1, 1);
-      dma_k(ktiles[1], pages_v);
-    }
-    if (ntiles > 2) raw_k = fetch_ids(2);
-    wait_dma();
-    __syncthreads();
-    scores(ktiles[0], s_cur);
-    ok_cur = p0.ok;
-    {
-      const int rel = rel_of(0);
-      float mx = kNegBig;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) mx = quarter_max(s_cur, q, rel, ok_cur, mx, std::true_type{});
-      fold_max(mx);
-    }
-    __syncthreads();  // every wave has read ktiles[0] before step 0 refills it
-    using F = std::false_type;
-    using T = std::true_type;
-    // Interior steps while tiles j and j+1 are interior and their pages all
-    // present, then steps whose next tile is masked (a missing page, an
-    // error case, sends the rest down the masked path).
-    const int last = ntiles - 1;
-    int j = 0;
-    for (; j + 1 < n_full && (ok_cur & pages_v.ok) == 0xF; ++j) step(j, F{}, T{});
-    for (; j < last; ++j) step(j, T{}, T{});
-    step(last, T{}, F{});
+    if (team == 0) run(std::integral_constant<int, 0>{});
+    else run(std::integral_constant<int, 1>{});
   }
 
   if (!row_ok) return;

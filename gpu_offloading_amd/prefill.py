@@ -12,7 +12,7 @@ append), so each request's keys are ``kv_len`` cached tokens of which the last
 FlashInfer's).
 
 ``plan`` is host work plus one small H2D copy: it reads the host index
-pointers, cuts every request's queries into 128-row tiles (tile tokens x the
+pointers, cuts every request's queries into 256-row tiles (tile tokens x the
 GQA group) ordered longest-first, and stages the work list.
 """
 from __future__ import annotations
@@ -26,6 +26,9 @@ import torch
 from . import _lib
 
 __all__ = ["BatchPrefillWithPagedKVCacheWrapper"]
+
+# Query rows (tokens x the GQA group) per work item of the prefill kernel.
+_TILE_ROWS = 256
 
 
 def _fail(msg: str) -> None:
@@ -103,7 +106,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         if num_kv_heads <= 0 or num_qo_heads % num_kv_heads:
             _fail("num_qo_heads must be a multiple of num_kv_heads")
         group = num_qo_heads // num_kv_heads
-        tile = 128 // group if group in (1, 2, 4, 8) else 1
+        tile = _TILE_ROWS // group if group in (1, 2, 4, 8) else 1
         q_lens = np.diff(qo.astype(np.int64)) if batch > 0 else np.zeros(0, np.int64)
         cap = int(np.sum((np.maximum(q_lens, 0) + tile - 1) // tile)) * 8 + 8
 
@@ -132,7 +135,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
     @staticmethod
     def _plan_capacity(q_lens: np.ndarray, group: int) -> int:
         """int32 entries to reserve for the plan image (16-byte multiple)."""
-        tile = 128 // group if group in (1, 2, 4, 8) else 1
+        tile = _TILE_ROWS // group if group in (1, 2, 4, 8) else 1
         ql = np.maximum(np.asarray(q_lens, np.int64), 0)
         cap = int(np.sum((ql + tile - 1) // tile)) * 8 + 8
         return (cap + 3) // 4 * 4

@@ -385,14 +385,15 @@ def test_prefill_plan_tiles_every_query_once_longest_first(lib):
     q_lens, kv_lens = [1, 17, 40, 64, 130, 0, 33], [1, 40, 40, 300, 130, 12, 1000]
     st, sched, rec, qo, kvi = _prefill_plan(lib, q_lens, kv_lens)
     assert st == 0, lib.kvc_last_error()
-    assert sched.tile_tokens == 32 and sched.total_q == sum(q_lens)
+    T = sched.tile_tokens                                         # 256 query rows / group 4
+    assert T == 64 and sched.total_q == sum(q_lens)
     assert (np.diff(rec[:, 6]) <= 0).all()                        # longest first
     for b, (ql, kl) in enumerate(zip(q_lens, kv_lens)):
         mine = rec[rec[:, 0] == b]
-        assert sorted(mine[:, 1].tolist()) == list(range(0, ql, 32))
+        assert sorted(mine[:, 1].tolist()) == list(range(0, ql, T))
         for r in mine:
             assert (r[2], r[3], r[4], r[5], r[7]) == (ql, kl, qo[b], kvi[b], kvi[b + 1] - kvi[b])
-            last = min(r[1] + 32, ql) - 1
+            last = min(r[1] + T, ql) - 1
             keys = max(0, min(last + kl - ql + 1, kl))
             assert r[6] == (keys + 63) // 64
     assert sched.max_key_tiles == rec[:, 6].max()
@@ -400,14 +401,14 @@ def test_prefill_plan_tiles_every_query_once_longest_first(lib):
     st, sched, rec, _, _ = _prefill_plan(lib, q_lens, kv_lens, causal=0)
     assert st == 0
     assert all(r[6] == (r[3] + 63) // 64 for r in rec)
-    # group 8 packs 16 tokens x 8 heads per tile
+    # group 8 packs 32 tokens x 8 heads per tile
     st, sched, rec, _, _ = _prefill_plan(lib, [100], [100], hq=16, hkv=2)
-    assert st == 0 and sched.tile_tokens == 16 and sched.num_items == 7
+    assert st == 0 and sched.tile_tokens == 32 and sched.num_items == 4
 
 
 def test_prefill_plan_reports_capacity_and_rejects_bad_input(lib):
     st, sched, _, _, _ = _prefill_plan(lib, [100, 40], [100, 40], cap=8)
-    assert st == 4 and sched.plan_ints == 8 * (4 + 2)
+    assert st == 4 and sched.plan_ints == 8 * (2 + 1)
     assert b"plan buffer too small" in lib.kvc_last_error()
     st, *_ = _prefill_plan(lib, [10], [10], hq=24, hkv=8)
     assert st == 2                                                 # group 3

@@ -61,7 +61,7 @@ def test_prefill_mixed_batch_gqa4(gpu):
     one-token chunk, partial last pages and query tiles that straddle both
     the chunk end and the causal diagonal."""
     w = _check(gpu, [1, 17, 40, 64, 130, 5, 33], [1, 40, 40, 300, 130, 133, 1000], 32, 8, 30)
-    assert w.schedule.tile_tokens == 32 and w.schedule.num_items == 1 + 1 + 2 + 2 + 5 + 1 + 2
+    assert w.schedule.tile_tokens == 64 and w.schedule.num_items == 1 + 1 + 1 + 1 + 3 + 1 + 1
 
 
 @pytest.mark.parametrize("group", [1, 2, 8])
