@@ -96,7 +96,7 @@ def parse_args():
                         "layer) instead of the fused append_and_decode")
     p.add_argument("--mode", default="step",
                    choices=["step", "copy", "decode2", "decode4", "append3", "prefill3",
-                            "xpacked", "offload", "swap5", "bs1"])
+                            "prefill_power", "xpacked", "offload", "swap5", "bs1"])
     return p.parse_args()
 
 
@@ -436,41 +436,110 @@ def prefill_flops(q_lens, kv_lens, hq, d, causal=True):
     return total
 
 
+def _prefill_problem(torch, seed, q_len, kv_len, hq=32, hkv=8, d=128):
+    """Eight requests of q_len queries over kv_len cached keys (the chunk's
+    own keys last), pages from a seeded permuted pool, planned causal."""
+    import numpy as np
+
+    from gpu_offloading_amd.prefill import BatchPrefillWithPagedKVCacheWrapper
+
+    q_lens, kv_lens = [q_len] * 8, [kv_len] * 8
+    kc, vc, _, w0 = build_paged(torch, kv_lens, hkv, d, seed + 11, hq=hq)
+    qo = np.arange(0, 9 * q_len, q_len, dtype=np.int32)
+    kvi = np.arange(0, 9 * (kv_len // 16), kv_len // 16, dtype=np.int32)
+    lpl = np.full(8, 16, np.int32)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 12)
+    q = torch.randn(8 * q_len, hq, d, device="cuda", generator=g).to(torch.bfloat16)
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1 << 20, dtype=torch.uint8, device="cuda"))
+    w.plan(torch.from_numpy(qo), torch.from_numpy(kvi), w0._indices, torch.from_numpy(lpl),
+           num_qo_heads=hq, num_kv_heads=hkv, head_dim_qk=d, page_size=16, causal=True,
+           q_data_type=torch.bfloat16)
+    out = torch.empty_like(q)
+    return (lambda: w.run(q, (kc, vc), out=out)), out, prefill_flops(q_lens, kv_lens, hq, d)
+
+
 def run_prefill(torch, seed, reps=10):
     """Paged-KV continuation prefill (the attention after the cfg3 append):
     8 requests x 2048-token chunks, Hq=32 / Hkv=8 / D=128, causal, over
     (a) the chunk alone (first chunk) and (b) a 2048-token cached prefix plus
     the chunk (second chunk).  Pages come from a seeded permuted pool."""
-    import numpy as np
-
-    from gpu_offloading_amd.prefill import BatchPrefillWithPagedKVCacheWrapper
-
-    hq, hkv, d = 32, 8, 128
     res = {}
     for name, q_len, kv_len in (("first_chunk", 2048, 2048), ("second_chunk", 2048, 4096)):
-        q_lens, kv_lens = [q_len] * 8, [kv_len] * 8
-        kc, vc, _, w0 = build_paged(torch, kv_lens, hkv, d, seed + 11, hq=hq)
-        qo = np.arange(0, 9 * q_len, q_len, dtype=np.int32)
-        kvi = np.arange(0, 9 * (kv_len // 16), kv_len // 16, dtype=np.int32)
-        lpl = np.full(8, 16, np.int32)
-        g = torch.Generator(device="cuda")
-        g.manual_seed(seed + 12)
-        q = torch.randn(8 * q_len, hq, d, device="cuda", generator=g).to(torch.bfloat16)
-        w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1 << 20, dtype=torch.uint8, device="cuda"))
-        w.plan(torch.from_numpy(qo), torch.from_numpy(kvi), w0._indices, torch.from_numpy(lpl),
-               num_qo_heads=hq, num_kv_heads=hkv, head_dim_qk=d, page_size=16, causal=True,
-               q_data_type=torch.bfloat16)
-        out = torch.empty_like(q)
-        t = _timed_rounds(torch, lambda: w.run(q, (kc, vc), out=out), reps)
-        f = prefill_flops(q_lens, kv_lens, hq, d)
+        fn, out, f = _prefill_problem(torch, seed, q_len, kv_len)
+        t = _timed_rounds(torch, fn, reps)
         assert torch.isfinite(out).all().item(), "non-finite prefill output"
         res[name] = {"q_len": q_len, "kv_len": kv_len, "requests": 8, "us": t * 1e6,
                      "TFLOPs": f / t / 1e12, "frac_of_peak": f / t / 1e12 / MFMA_BF16_PEAK_TFLOPS,
                      "algorithmic_flops": f}
         log(f"prefill {name}: 8 x {q_len} queries over {kv_len} keys, {t * 1e6:.1f} us, "
             f"{f / t / 1e12:.1f} TFLOP/s ({f / t / 1e12 / MFMA_BF16_PEAK_TFLOPS:.1%} of bf16 MFMA peak)")
-        del kc, vc, q, w0, w, out
+        del fn, out
         torch.cuda.empty_cache()
+    return res
+
+
+def _smi_power_clock():
+    """(socket power W, mean GFX clock MHz over the XCDs) from `amd-smi
+    metric -p -c`, or (None, None) when the tool is missing."""
+    import subprocess
+
+    try:
+        txt = subprocess.run(["amd-smi", "metric", "-g", "0", "-p", "-c"], capture_output=True,
+                             text=True, timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None, None
+    power, clocks, section = None, [], ""
+    for line in txt.splitlines():
+        key, _, val = line.strip().partition(":")
+        if not val.strip():
+            section = key
+            continue
+        if key == "SOCKET_POWER":
+            power = float(val.split()[0])
+        elif key == "CLK" and section.startswith("GFX_"):
+            clocks.append(float(val.split()[0]))
+    return power, (sum(clocks) / len(clocks) if clocks else None)
+
+
+def run_prefill_power(torch, seed, seconds=6.0, q_len=2048, kv_len=4096):
+    """The (second-chunk) prefill launched back to back for `seconds` while the
+    board's socket power and GFX clocks are sampled (amd-smi), and the bf16
+    MFMA peak at the sampled clock (1,024 SIMDs x 1,024 FLOP per cycle)."""
+    import threading
+
+    fn, out, f = _prefill_problem(torch, seed, q_len, kv_len)
+    _round_times(torch, fn, 3, rounds=1, warm_s=0.5)
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        while not stop.wait(0.5):
+            samples.append(_smi_power_clock())
+
+    th = threading.Thread(target=sampler)
+    th.start()
+    n, t0 = 0, time.perf_counter()
+    e0, e1 = _events(torch)
+    e0.record()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            fn()
+        n += 20
+        torch.cuda.synchronize()
+    e1.record()
+    torch.cuda.synchronize()
+    stop.set()
+    th.join()
+    t = e0.elapsed_time(e1) * 1e-3 / n
+    got = [x for x in samples[1:] if x[0] is not None and x[1] is not None]
+    power = sorted(p for p, _ in got)[len(got) // 2] if got else None
+    clock = sorted(c for _, c in got)[len(got) // 2] if got else None
+    peak = 1024 * 1024 * clock * 1e6 / 1e12 if clock else None
+    res = {"launches": n, "us": t * 1e6, "TFLOPs": f / t / 1e12, "samples": len(got),
+           "socket_power_W": power, "gfx_clock_MHz": clock, "bf16_peak_at_clock_TFLOPs": peak,
+           "frac_of_peak_at_clock": f / t / 1e12 / peak if peak else None}
+    log(f"prefill {q_len} over {kv_len} sustained: {t * 1e6:.1f} us, {f / t / 1e12:.1f} TFLOP/s, "
+        f"socket {power} W, GFX {clock} MHz")
     return res
 
 
@@ -1160,6 +1229,10 @@ def main():
     if args.mode == "prefill3":
         print(json.dumps({"mode": "prefill3", **run_prefill(torch, args.seed)}), flush=True)
         return
+    if args.mode == "prefill_power":
+        print(json.dumps({"mode": "prefill_power", **run_prefill_power(torch, args.seed)}),
+              flush=True)
+        return
     if args.mode == "bs1":
         print(json.dumps({"mode": "bs1", **run_small_batch(torch, args.seed)}), flush=True)
         return
@@ -1185,6 +1258,8 @@ def main():
             extra["cfg5_swap"][f"swap_{k}_frac_of_link"] = round(
                 extra["cfg5_swap"][f"swap_{k}_GBps"] / peak, 3)
         extra["f2_continuation_prefill"] = run_prefill(torch, args.seed)
+        extra["f2_continuation_prefill"]["second_chunk_sustained"] = run_prefill_power(
+            torch, args.seed, seconds=4.0)
         extra["f3_xpacked"] = run_xpacked(torch, args.seed)
         extra["f4_offload"] = run_offload(torch, args.seed)
         extra["bs1_latency"] = run_small_batch(torch, args.seed)

@@ -448,12 +448,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
     if (kTeam == 0) {
       // Team 0 stages nothing; it only needs each tile's present pages for
       // its VALU phase, resolved one tile ahead after that phase.
-      RawIds raw = fetch_ids(0);
-      int ok_cur = resolve(raw, 0).ok;   // tile j's, from slot 2j+1 on
-      raw = fetch_ids(1);
+      const RawIds raw0 = fetch_ids(0);
+      RawIds raw = fetch_ids(1);
       __syncthreads();
       mfma(0, no{}, yes{});
       __syncthreads();
+      int ok_cur = resolve(raw0, 0).ok;  // tile j's, from slot 2j+1 on
       valu_phase(0, ok_cur);
       ok_cur = resolve(raw, 1).ok;
       raw = fetch_ids(2);
@@ -472,11 +472,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
     } else {
       // Team 1 stages K_{j+1} and V_j at the start of slot 2j, from pages
       // resolved two tiles ahead, and waits for them at the end of slot 2j+1.
-      RawIds raw = fetch_ids(0);
-      Pages pv = resolve(raw, 0);        // tile j's pages, at slot 2j
-      raw = fetch_ids(1);
-      Pages pk = resolve(raw, 1);        // tile j+1's
-      raw = fetch_ids(2);
+      // The first three tiles' page ids are fetched together (one memory
+      // round trip before the first K tile can be requested).
+      const RawIds raw0 = fetch_ids(0), raw1 = fetch_ids(1);
+      RawIds raw = fetch_ids(2);
+      Pages pv = resolve(raw0, 0);       // tile j's pages, at slot 2j
+      Pages pk = resolve(raw1, 1);       // tile j+1's
       int ok_prev = 0;                   // tile j-1's present pages
       // After slot 2j's loads are issued: resolve tile j+2, fetch tile j+3's
       // page ids and shift the window.
