@@ -5,11 +5,12 @@
 // continuation prefills (src/MoE/moe_engine.py:1733-1751, 3710-3727,
 // 3939-3941).
 //
-// Work item = (request, tile of kTileRows query rows) x one KV head.  A query
+// Work unit = (request, tile of kTileRows query rows) x one KV head.  A query
 // row is a (token, query head) pair: the `group` query heads that share a KV
 // head are packed into the rows of one tile, so every K/V tile staged in LDS
 // serves all of them (GQA reuse).  The eight waves of a workgroup own 32 rows
-// each; the workgroup walks the request's keys in tiles of 64.
+// each and walk the request's keys in tiles of 64.  At most one workgroup
+// per CU is launched; each runs a list of units made by the host plan.
 //
 // Per key tile, per wave, with v_mfma_f32_32x32x16_bf16 (A: lane l = row l%32,
 // k = 8(l/32)..+7; B: lane l = column l%32, same k; C: acc[4i+j] = row
@@ -39,6 +40,7 @@
 #include "kvc_common.h"
 
 #include <algorithm>
+#include <queue>
 #include <cmath>
 #include <type_traits>
 #include <vector>
@@ -83,7 +85,8 @@ struct PrefillArgs {
   int64_t num_blocks;
   const int32_t* indices;
   int64_t num_indices;
-  const int4* items;       // [N][2]: (request, first query, q_len, kv_len),
+  const int2* wg_units;    // [workgroups]: (first unit, units)
+  const int4* units;       // [U][2]: (KV head, first query, q_len, kv_len),
                            //         (q offset, page offset, key tiles, pages)
   int32_t num_kv_heads;
   int32_t causal;
@@ -138,17 +141,21 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 // more than 2^8, P packed to bf16 with v_cvt_pk_bf16_f32 and summed from the
 // packed pairs with v_dot2_f32_bf16, the row max exchanged between the lane
 // halves with v_permlane32_swap.
+//
+// The host plan gives each workgroup a list of units (the list scheduling a
+// dispatcher would do, made explicit so that a unit's first loads can be
+// issued during the previous unit: its record, its first page ids and, by
+// team 1 in the previous unit's slot 2n, its first K tile).
+
+// A work unit's record: (KV head, first query, q_len, kv_len, q offset, page
+// offset, key tiles, pages) of one query tile of one request.
+struct Unit { int h, tok0, q_len, kv_len, q_off, page_off, ntiles, npages; };
+
 template <int G>
 __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int kTokPerWave = kWaveRows / G;
   __shared__ KTile ktiles[2];
   __shared__ VTile vtiles[2];
-
-  const int h = blockIdx.y;
-  const int4 it0 = a.items[2 * blockIdx.x];
-  const int4 it1 = a.items[2 * blockIdx.x + 1];
-  const int tok0 = it0.y, q_len = it0.z, kv_len = it0.w;
-  const int q_off = it1.x, page_off = it1.y, ntiles = it1.z, npages = it1.w;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
   const int team = wave >> 2;
@@ -157,39 +164,70 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
   const int r = lane & 31;
   const int half = lane >> 5;
   const int g = r % G;
-  const int tok = tok0 + wave * kTokPerWave + r / G;
-  const bool row_ok = tok < q_len;
-  // Last key this row may see (inclusive).
-  const int limit = !row_ok ? -1 : a.causal ? min(tok + kv_len - q_len, kv_len - 1) : kv_len - 1;
-  const int hq = h * G + g;
   const int Hq = a.num_kv_heads * G;
 
-  // Q as the B operand of S^T = K Q^T: k-step ks covers head dims
+  // This workgroup's units, in order: records [first, first + count).
+  const int2 span = a.wg_units[blockIdx.x];
+  const int u_first = __builtin_amdgcn_readfirstlane(span.x);
+  const int u_count = __builtin_amdgcn_readfirstlane(span.y);
+  // A unit's record as loaded (VGPRs, no wait) and as used (SGPRs).
+  struct RawUnit { int4 x, y; };
+  auto fetch_unit = [&](int u) __attribute__((always_inline)) {
+    return RawUnit{a.units[2 * u], a.units[2 * u + 1]};
+  };
+  auto to_unit = [](const RawUnit& t) __attribute__((always_inline)) {
+    auto rfl = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
+    return Unit{rfl(t.x.x), rfl(t.x.y), rfl(t.x.z), rfl(t.x.w),
+                rfl(t.y.x), rfl(t.y.y), rfl(t.y.z), rfl(t.y.w)};
+  };
+  // Q of a unit as the B operand of S^T = K Q^T: k-step ks covers head dims
   // 16ks .. 16ks+15, lane half h the dims 16ks + 8h .. +7.
-  bf16x8_t qb[kD / 16];
-  {
-    const int t = row_ok ? tok : 0;
-    const uint16_t* qp = a.q + int64_t(q_off + t) * a.q_stride + int64_t(hq) * kD + 8 * half;
+  auto load_q = [&](const Unit& U, bf16x8_t (&dst)[kD / 16]) __attribute__((always_inline)) {
+    const int t = U.tok0 + wave * kTokPerWave + r / G;
+    const bool ok = t < U.q_len;
+    const uint16_t* qp = a.q + int64_t(U.q_off + (ok ? t : 0)) * a.q_stride +
+                         int64_t(U.h * G + g) * kD + 8 * half;
 #pragma unroll
     for (int ks = 0; ks < kD / 16; ++ks) {
-      const uint4 v = row_ok ? *reinterpret_cast<const uint4*>(qp + 16 * ks) : make_uint4(0, 0, 0, 0);
-      qb[ks] = as_bf16x8(v);
+      const uint4 v = ok ? *reinterpret_cast<const uint4*>(qp + 16 * ks) : make_uint4(0, 0, 0, 0);
+      dst[ks] = as_bf16x8(v);
     }
-  }
+  };
 
-  const int64_t head_off = int64_t(h) * kD;
+  // The current unit and this lane's row in it.
+  Unit cu = to_unit(fetch_unit(u_first));
+  int tok = 0, limit = -1, hq = 0, n_full = 0;
+  bool row_ok = false;
+  const int32_t last_index = int32_t(min(a.num_indices - 1, int64_t(INT32_MAX)));
+  auto set_unit = [&](const Unit& U) __attribute__((always_inline)) {
+    cu = U;
+    tok = U.tok0 + wave * kTokPerWave + r / G;
+    row_ok = tok < U.q_len;
+    // Last key this row may see (inclusive).
+    limit = !row_ok ? -1 : a.causal ? min(tok + U.kv_len - U.q_len, U.kv_len - 1) : U.kv_len - 1;
+    hq = U.h * G + g;
+    // Tiles [0, n_full) are interior for every row of the workgroup (all
+    // its rows see keys up to at least its first token's limit).
+    const int lim_lo = a.causal ? U.tok0 + U.kv_len - U.q_len : U.kv_len - 1;
+    n_full = max(0, min(U.ntiles, (lim_lo + 1) / kKeys));
+  };
+  set_unit(cu);
+  bf16x8_t qb[kD / 16];
+  load_q(cu, qb);
+
   const char* kbase = reinterpret_cast<const char*>(a.k_cache);
   const char* vbase = reinterpret_cast<const char*>(a.v_cache);
   const int64_t tok_bytes = a.token_stride * 2;
   // Direct-to-LDS staging: this wave's load i fetches keys 4i .. 4i+3 of its
   // page, lane L key 4i + L/16, the chunk whose swizzled slot is L%16 (K and
-  // V each with their own swizzle).
+  // V each with their own swizzle), at these offsets from the unit's head
+  // slice of the page.
   uint32_t lane_k[4], lane_v[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int key = 4 * i + (lane >> 4);
-    lane_k[i] = uint32_t(key * tok_bytes + (head_off + ((lane & 15) ^ (key & 15)) * 8) * 2);
-    lane_v[i] = uint32_t(key * tok_bytes + (head_off + ((lane & 15) ^ (4 * (key & 3))) * 8) * 2);
+    lane_k[i] = uint32_t(key * tok_bytes + ((lane & 15) ^ (key & 15)) * 16);
+    lane_v[i] = uint32_t(key * tok_bytes + ((lane & 15) ^ (4 * (key & 3))) * 16);
   }
   // Every global_load_lds of this wave has written LDS (vmcnt 0).
   auto wait_dma = []() __attribute__((always_inline)) { __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); };
@@ -198,26 +236,26 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
   // clamped address, one load per tile, fetched well before the K/V loads
   // need them.  Index arithmetic is 32-bit (the host keeps every page index
   // below 2^31).
-  const int32_t last_index = int32_t(min(a.num_indices - 1, int64_t(INT32_MAX)));
   const int32_t num_blocks32 = int32_t(min(a.num_blocks, int64_t(INT32_MAX)));
   struct RawIds { int32_t v; };
-  auto fetch_ids = [&](int tile) __attribute__((always_inline)) {
-    return RawIds{a.indices[min(page_off + tile * 4 + (lane & 3), last_index)]};
+  auto fetch_ids = [&](const Unit& U, int tile) __attribute__((always_inline)) {
+    return RawIds{a.indices[min(U.page_off + tile * 4 + (lane & 3), last_index)]};
   };
-  // Byte offset of this wave's page of a tile (the host keeps a block stride
-  // under 4 GiB) and the tile's present pages: bit u of `ok` says page u is
+  // Byte offset of this wave's page of a tile, at the unit's head (the host
+  // keeps a block stride under 4 GiB), and the tile's present pages: bit u of `ok` says page u is
   // real (inside the request and the cache); the others read block 0 and
   // are masked.  Pages [0, pages_here) of the item exist in the request and
   // the index array; a present page also needs an id in [0, num_blocks).  The
   // four tests run on lanes 0..3 at once and one ballot collects them.
   const uint32_t blk32 = uint32_t(a.block_stride * 2);
   struct Pages { uint64_t off; int ok; };
-  const int pages_here = min(npages, last_index - page_off + 1);
-  auto resolve = [&](const RawIds& t, int tile) __attribute__((always_inline)) {
+  auto resolve = [&](const Unit& U, const RawIds& t, int tile) __attribute__((always_inline)) {
+    const int pages_here = min(U.npages, last_index - U.page_off + 1);
     const bool good = (tile * 4 + (lane & 3) < pages_here) & (uint32_t(t.v) < uint32_t(num_blocks32));
     const int ok = int(__builtin_amdgcn_ballot_w64(good) & 0xF);
     const int32_t v = good ? t.v : 0;
-    return Pages{uint64_t(uint32_t(__builtin_amdgcn_readlane(v, pw_idx))) * blk32, ok};
+    return Pages{uint64_t(uint32_t(__builtin_amdgcn_readlane(v, pw_idx))) * blk32 +
+                     uint32_t(U.h * kD * 2), ok};
   };
   // Direct loads from memory into LDS (global_load_lds_dwordx4 and
   // buffer_load_dwordx4 ... lds, one 16-byte chunk per lane, lane L at LDS
@@ -233,13 +271,22 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
   };
   // K: one instruction of a wave fills 1 KB of LDS (keys 4i .. 4i+3 of the
   // wave's page): one block address per wave and tile.
+  // A wave-uniform 64-bit value as an SGPR pair (the page offsets are
+  // uniform, but the compiler may keep them in VGPRs).
+  auto sgpr64 = [](uint64_t v) __attribute__((always_inline)) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
+    return (uint64_t(hi) << 32) | lo;
+  };
   auto dma_k = [&](KTile& buf, const Pages& p) __attribute__((always_inline)) {
-    const char* blk = kbase + p.off;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-                   :: "s"(lds_addr(buf.b + (pw_idx * kPage + 4 * i) * kKRow)), "v"(lane_k[i]),
-                      "s"(blk) : "memory");
+    const uint64_t blk = sgpr64(reinterpret_cast<uint64_t>(kbase + p.off));
+    asm volatile("s_mov_b32 m0, %0\n\t"
+                 "global_load_lds_dwordx4 %1, %5\n\ts_add_u32 m0, m0, 0x400\n\t"
+                 "global_load_lds_dwordx4 %2, %5\n\ts_add_u32 m0, m0, 0x400\n\t"
+                 "global_load_lds_dwordx4 %3, %5\n\ts_add_u32 m0, m0, 0x400\n\t"
+                 "global_load_lds_dwordx4 %4, %5"
+                 :: "s"(lds_addr(buf.b + pw_idx * kPage * kKRow)), "v"(lane_k[0]), "v"(lane_k[1]),
+                    "v"(lane_k[2]), "v"(lane_k[3]), "s"(blk) : "memory", "scc");
   };
   // V goes into LDS the same way, through a buffer load bounded to the
   // page's valid tokens: lanes past kv_len or in a missing page get zeros
@@ -248,7 +295,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
   // holding such keys are processed with the per-key tests, which never
   // read its score.
   const int page_bytes = kPage * int(tok_bytes);  // under 2 GiB (host check)
-  auto dma_v = [&](VTile& buf, const Pages& p, int tile) __attribute__((always_inline)) {
+  auto dma_v = [&](VTile& buf, const Pages& p, int kv_len, int tile) __attribute__((always_inline)) {
     const bool real = (p.ok >> pw_idx) & 1;
     int bytes = real ? page_bytes : 0;
     if ((tile + 1) * kKeys > kv_len) {
@@ -259,11 +306,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
     const i32x4_t rsrc = {__builtin_amdgcn_readfirstlane(int(uint32_t(blk))),
                           __builtin_amdgcn_readfirstlane(int(uint32_t(blk >> 32) & 0xFFFF)),
                           __builtin_amdgcn_readfirstlane(bytes), kBufferRsrcWord3};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                   :: "s"(lds_addr(buf.b + (pw_idx * kPage + 4 * i) * kKRow)), "v"(lane_v[i]),
-                      "s"(rsrc) : "memory");
+    asm volatile("s_mov_b32 m0, %0\n\t"
+                 "buffer_load_dwordx4 %1, %5, 0 offen lds\n\ts_add_u32 m0, m0, 0x400\n\t"
+                 "buffer_load_dwordx4 %2, %5, 0 offen lds\n\ts_add_u32 m0, m0, 0x400\n\t"
+                 "buffer_load_dwordx4 %3, %5, 0 offen lds\n\ts_add_u32 m0, m0, 0x400\n\t"
+                 "buffer_load_dwordx4 %4, %5, 0 offen lds"
+                 :: "s"(lds_addr(buf.b + pw_idx * kPage * kKRow)), "v"(lane_v[0]), "v"(lane_v[1]),
+                    "v"(lane_v[2]), "v"(lane_v[3]), "s"(rsrc) : "memory", "scc");
   };
 
   // V tiles start as zeros: should a bounded load leave the LDS rows of
@@ -338,12 +387,6 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
   auto visible = [&](int rel, int ok, int kb, int e) __attribute__((always_inline)) {
     return (32 * kb + 8 * (e >> 2) + (e & 3)) <= rel && ((ok >> (2 * kb + (e >> 3))) & 1);
   };
-  // Tiles [0, n_full) are interior for every row of the workgroup when all
-  // their pages are present: all its rows see keys up to at least lim_lo
-  // (its first token's limit).
-  const int lim_lo = a.causal ? tok0 + kv_len - q_len : kv_len - 1;
-  const int n_full = max(0, min(ntiles, (lim_lo + 1) / kKeys));
-
   // M_j: O += P_{j-1} V_{j-1} (do_o), then S_j = K_j Q (do_s), each MFMA's
   // LDS operand read four MFMAs ahead.
   auto mfma_phase = [&](int j, auto do_o_c, auto do_s_c) __attribute__((always_inline)) {
@@ -430,12 +473,46 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
     l_half += sum0 + sum1;
   };
 
-  // Slots 2j and 2j+1 (each ends on a workgroup barrier): team 0 runs M_j
-  // then X_j, team 1 runs X_{j-1} then M_j.  Each team has its own copy of the
-  // code (the team is a compile-time constant in `run`), with the first and
-  // last tiles peeled, so the loop body is straight-line code in which O, S
-  // and P keep their registers; the teams only have to meet the same
-  // barriers, not the same instructions.
+  // The unit's output rows: O / l in bf16 and, when asked, the natural-log
+  // log-sum-exp; then the running state starts over for the next unit.
+  auto finish_unit = [&]() __attribute__((always_inline)) {
+    const float l_run = l_half + __shfl_xor(l_half, 32);
+    if (row_ok) {
+      // O^T column r = this row; entry (db, 4i+j) = head dim 32db + 8i + 4half + j.
+      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+      uint16_t* dst = a.out + int64_t(cu.q_off + tok) * a.out_stride + int64_t(hq) * kD + 4 * half;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          *reinterpret_cast<uint2*>(dst + 32 * db + 8 * i) =
+              make_uint2(pack_bf16(o[db][4 * i] * inv, o[db][4 * i + 1] * inv),
+                         pack_bf16(o[db][4 * i + 2] * inv, o[db][4 * i + 3] * inv));
+        }
+      if (a.lse && half == 0)
+        a.lse[int64_t(cu.q_off + tok) * Hq + hq] =
+            l_run > 0.f ? (m_run + fast_log2(l_run)) * kLn2 : -INFINITY;
+    }
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[db][e] = 0.f;
+    m_run = kNegBig;
+    l_half = 0.f;
+  };
+
+  // Per unit with n key tiles, slots 2j and 2j+1 (each ends on a workgroup
+  // barrier): team 0 runs M_j then X_j, team 1 runs X_{j-1} then M_j, for j
+  // = 0 .. n (M_0 without O, M_n without S).  Each team has its own copy of
+  // the code (the team is a compile-time constant in `run`), with the first
+  // and last tiles peeled, so the loop body is straight-line code in which
+  // O, S and P keep their registers; the teams only have to meet the same
+  // barriers, not the same instructions.  While a unit runs, the next one's
+  // record and first page ids are fetched, its Q is loaded once this unit's
+  // last S_j is done, and team 1 stages its first K tile in slot 2n.  A
+  // unit whose first K tile was not staged that way (the workgroup's first,
+  // or one after a unit without key tiles) starts with a staging step of its
+  // own.
   using yes = std::true_type;
   using no = std::false_type;
   auto run = [&](auto team_c) __attribute__((always_inline)) {
@@ -445,100 +522,143 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
       mfma_phase(j, do_o_c, do_s_c);
       __builtin_amdgcn_s_setprio(0);
     };
-    if (kTeam == 0) {
-      // Team 0 stages nothing; it only needs each tile's present pages for
-      // its VALU phase, resolved one tile ahead after that phase.
-      const RawIds raw0 = fetch_ids(0);
-      RawIds raw = fetch_ids(1);
-      __syncthreads();
-      mfma(0, no{}, yes{});
-      __syncthreads();
-      int ok_cur = resolve(raw0, 0).ok;  // tile j's, from slot 2j+1 on
-      valu_phase(0, ok_cur);
-      ok_cur = resolve(raw, 1).ok;
-      raw = fetch_ids(2);
-      __syncthreads();
-      for (int j = 1; j < ntiles; ++j) {
-        mfma(j, yes{}, yes{});
-        __syncthreads();
-        valu_phase(j, ok_cur);
-        ok_cur = resolve(raw, j + 1).ok;
-        raw = fetch_ids(j + 2);
-        __syncthreads();
+    Unit nu = u_count > 1 ? to_unit(fetch_unit(u_first + 1)) : cu;  // the next unit
+    RawUnit nnu{};                                                   // the one after
+    RawIds c0 = fetch_ids(cu, 0), c1 = fetch_ids(cu, 1);     // current unit's tiles 0, 1
+    RawIds n0{0}, n1{0}, n2{0};                             // next unit's tiles 0..2
+    bool staged = false;      // the current unit's K_0 is in ktiles[0] (team 1 state too)
+    Pages pv{0, 0}, pk{0, 0};  // team 1: pages of tiles j and j+1
+    RawIds raw{0};             // team 1: ids of tile j+2; team 0: of tile j+1
+    // After unit k's own first loads: the next unit's page ids and the
+    // record of the unit after it.
+    auto prefetch_next = [&](int k) __attribute__((always_inline)) {
+      if (k + 1 < u_count) {
+        n0 = fetch_ids(nu, 0);
+        n1 = fetch_ids(nu, 1);
+        n2 = fetch_ids(nu, 2);
+        if (k + 2 < u_count) nnu = fetch_unit(u_first + k + 2);
       }
-      mfma(ntiles, yes{}, no{});
-      __syncthreads();
-      __syncthreads();
-    } else {
-      // Team 1 stages K_{j+1} and V_j at the start of slot 2j, from pages
-      // resolved two tiles ahead, and waits for them at the end of slot 2j+1.
-      // The first three tiles' page ids are fetched together (one memory
-      // round trip before the first K tile can be requested).
-      const RawIds raw0 = fetch_ids(0), raw1 = fetch_ids(1);
-      RawIds raw = fetch_ids(2);
-      Pages pv = resolve(raw0, 0);       // tile j's pages, at slot 2j
-      Pages pk = resolve(raw1, 1);       // tile j+1's
-      int ok_prev = 0;                   // tile j-1's present pages
-      // After slot 2j's loads are issued: resolve tile j+2, fetch tile j+3's
-      // page ids and shift the window.
-      auto advance = [&](int j) __attribute__((always_inline)) {
-        const Pages pn = resolve(raw, j + 2);
-        raw = fetch_ids(j + 3);
-        ok_prev = pv.ok;
-        pv = pk;
-        pk = pn;
-      };
-      dma_k(ktiles[0], pv);
-      wait_dma();
-      __syncthreads();
-      if (1 < ntiles) dma_k(ktiles[1], pk);
-      dma_v(vtiles[0], pv, 0);
-      advance(0);
-      __syncthreads();
-      mfma(0, no{}, yes{});
-      wait_dma();
-      __syncthreads();
-      for (int j = 1; j < ntiles; ++j) {
-        if (j + 1 < ntiles) dma_k(ktiles[(j + 1) & 1], pk);
-        dma_v(vtiles[j & 1], pv, j);
-        valu_phase(j - 1, ok_prev);
-        advance(j);
-        __syncthreads();
-        mfma(j, yes{}, yes{});
-        wait_dma();
-        __syncthreads();
+    };
+    for (int k = 0; k < u_count; ++k) {
+      const bool has_next = k + 1 < u_count;
+      const int n = cu.ntiles;
+      if (n > 0) {
+        if (kTeam == 0) {
+          // Team 0 stages nothing; it only needs each tile's present pages
+          // for its VALU phase, resolved one tile ahead after that phase.
+          if (!staged) __syncthreads();
+          mfma(0, no{}, yes{});
+          __syncthreads();
+          int ok_cur = resolve(cu, c0, 0).ok;  // tile j's, from slot 2j+1 on
+          valu_phase(0, ok_cur);
+          ok_cur = resolve(cu, c1, 1).ok;
+          raw = fetch_ids(cu, 2);
+          prefetch_next(k);
+          __syncthreads();
+          for (int j = 1; j < n; ++j) {
+            mfma(j, yes{}, yes{});
+            __syncthreads();
+            valu_phase(j, ok_cur);
+            ok_cur = resolve(cu, raw, j + 1).ok;
+            raw = fetch_ids(cu, j + 2);
+            __syncthreads();
+          }
+          // Q is not read again in this unit: the next unit's goes into its
+          // registers two slots before that unit's first MFMA phase.
+          if (has_next) load_q(nu, qb);
+          mfma(n, yes{}, no{});
+          __syncthreads();
+          finish_unit();
+          __syncthreads();
+        } else {
+          // Team 1 stages K_{j+1} and V_j at the start of slot 2j, from
+          // pages resolved two tiles ahead, and waits for them at the end of
+          // slot 2j+1.
+          int ok_prev = 0;                     // tile j-1's present pages
+          // After slot 2j's loads are issued: resolve tile j+2, fetch tile
+          // j+3's page ids and shift the window.
+          auto advance = [&](int j) __attribute__((always_inline)) {
+            const Pages pn = resolve(cu, raw, j + 2);
+            raw = fetch_ids(cu, j + 3);
+            ok_prev = pv.ok;
+            pv = pk;
+            pk = pn;
+          };
+          if (!staged) {
+            raw = fetch_ids(cu, 2);
+            pv = resolve(cu, c0, 0);
+            pk = resolve(cu, c1, 1);
+            dma_k(ktiles[0], pv);
+            wait_dma();
+            __syncthreads();
+          }
+          if (1 < n) dma_k(ktiles[1], pk);
+          dma_v(vtiles[0], pv, cu.kv_len, 0);
+          advance(0);
+          prefetch_next(k);
+          __syncthreads();
+          mfma(0, no{}, yes{});
+          wait_dma();
+          __syncthreads();
+          for (int j = 1; j < n; ++j) {
+            if (j + 1 < n) dma_k(ktiles[(j + 1) & 1], pk);
+            dma_v(vtiles[j & 1], pv, cu.kv_len, j);
+            valu_phase(j - 1, ok_prev);
+            advance(j);
+            __syncthreads();
+            mfma(j, yes{}, yes{});
+            wait_dma();
+            __syncthreads();
+          }
+          valu_phase(n - 1, ok_prev);
+          // Q is not read again in this unit (its last S_j was in slot
+          // 2n-1): the next unit's goes into its registers, waited for with
+          // this slot's loads.  The next unit's first K tile goes into
+          // ktiles[0], last read in slot 2n-1 or earlier.
+          if (has_next) load_q(nu, qb);
+          if (has_next && nu.ntiles > 0) {
+            pv = resolve(nu, n0, 0);
+            pk = resolve(nu, n1, 1);
+            raw = n2;
+            dma_k(ktiles[0], pv);
+          }
+          __syncthreads();
+          mfma(n, yes{}, no{});
+          wait_dma();
+          __syncthreads();
+          finish_unit();
+        }
+      } else {
+        prefetch_next(k);
+        if (has_next) load_q(nu, qb);
+        finish_unit();
       }
-      valu_phase(ntiles - 1, ok_prev);
-      __syncthreads();
-      mfma(ntiles, yes{}, no{});
-      __syncthreads();
+      if (has_next) {
+        staged = n > 0 && nu.ntiles > 0;
+        set_unit(nu);
+        if (k + 2 < u_count) nu = to_unit(nnu);
+        c0 = n0;
+        c1 = n1;
+      }
     }
   };
-  if (ntiles > 0) {
-    if (team == 0) run(std::integral_constant<int, 0>{});
-    else run(std::integral_constant<int, 1>{});
-  }
-
-  if (!row_ok) return;
-  const float l_run = l_half + __shfl_xor(l_half, 32);
-  // O^T column r = this row; entry (db, 4i+j) = head dim 32db + 8i + 4half + j.
-  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-  uint16_t* dst = a.out + int64_t(q_off + tok) * a.out_stride + int64_t(hq) * kD + 4 * half;
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<uint2*>(dst + 32 * db + 8 * i) =
-          make_uint2(pack_bf16(o[db][4 * i] * inv, o[db][4 * i + 1] * inv),
-                     pack_bf16(o[db][4 * i + 2] * inv, o[db][4 * i + 3] * inv));
-    }
-  if (a.lse && half == 0)
-    a.lse[int64_t(q_off + tok) * Hq + hq] = l_run > 0.f ? (m_run + fast_log2(l_run)) * kLn2 : -INFINITY;
+  if (team == 0) run(std::integral_constant<int, 0>{});
+  else run(std::integral_constant<int, 1>{});
 }
 
 template <int G>
-void launch(const PrefillArgs& a, int items, int hkv, hipStream_t s) {
-  prefill_mfma_kernel<G><<<dim3(unsigned(items), unsigned(hkv)), kThreads, 0, s>>>(a);
+void launch(const PrefillArgs& a, int workgroups, hipStream_t s) {
+  prefill_mfma_kernel<G><<<dim3(unsigned(workgroups)), kThreads, 0, s>>>(a);
+}
+
+// Persistent workgroups: at most one per CU of an MI355X (256), each running
+// a list of units; the plan image is the workgroups' (first unit, units)
+// table, padded to 4 int32, then the unit records.
+constexpr int64_t kMaxWorkgroups = 256;
+int64_t plan_workgroups(int64_t items, int hkv) { return std::min(kMaxWorkgroups, items * hkv); }
+int64_t plan_table_ints(int64_t workgroups) { return (2 * workgroups + 3) / 4 * 4; }
+int64_t plan_ints_for(int64_t items, int hkv) {
+  return plan_table_ints(plan_workgroups(items, hkv)) + items * hkv * kItemInts;
 }
 
 }  // namespace
@@ -602,7 +722,7 @@ extern "C" int kvc_prefill_plan(const int32_t* qo_indptr_host, const int32_t* kv
   sched->num_items = int32_t(n);
   sched->total_q = int32_t(std::min<int64_t>(total_q, INT32_MAX));
   sched->max_key_tiles = max_tiles;
-  sched->plan_ints = n * kItemInts;
+  sched->plan_ints = plan_ints_for(n, num_kv_heads);
   KVC_REQUIRE(plan_host && plan_capacity >= sched->plan_ints, KVC_ERR_WORKSPACE,
               "plan buffer too small: need " + std::to_string(sched->plan_ints) + " int32");
   // Longest items first: the causal tail of short tiles fills the gaps.
@@ -611,8 +731,43 @@ extern "C" int kvc_prefill_plan(const int32_t* qo_indptr_host, const int32_t* kv
   std::stable_sort(order.begin(), order.end(), [&](int64_t x, int64_t y) {
     return rec[x * kItemInts + 6] > rec[y * kItemInts + 6];
   });
-  for (int64_t i = 0; i < n; ++i)
-    std::copy_n(rec.data() + order[i] * kItemInts, kItemInts, plan_host + i * kItemInts);
+  // Units (item, KV head) in the order a grid of (items, heads) workgroups
+  // would be dispatched: head-major, items longest first.  The hardware
+  // hands workgroup w to XCD w % 8 and each XCD's next workgroup to its
+  // first free CU; the plan replays that list scheduling with each unit's
+  // cost taken as its key tiles + 2, assigning unit d to a workgroup of XCD
+  // d % 8 (workgroup b runs on XCD b % 8), so the units of one request and
+  // head still run side by side on one XCD and share its L2.
+  const int64_t units = n * num_kv_heads;
+  const int64_t W = plan_workgroups(n, num_kv_heads);
+  const int groups = (W % 8 == 0) ? 8 : 1;
+  std::vector<std::vector<int64_t>> lists(W);
+  {
+    typedef std::pair<int64_t, int64_t> Slot;  // (load, workgroup)
+    std::vector<std::priority_queue<Slot, std::vector<Slot>, std::greater<Slot>>> free_at(groups);
+    for (int64_t b = 0; b < W; ++b) free_at[b % groups].push(Slot(0, b));
+    for (int64_t d = 0; d < units; ++d) {
+      auto& q = free_at[d % groups];
+      const Slot sl = q.top();
+      q.pop();
+      lists[sl.second].push_back(d);
+      const int64_t item = order[d % n];
+      q.push(Slot(sl.first + rec[item * kItemInts + 6] + 2, sl.second));
+    }
+  }
+  const int64_t table = plan_table_ints(W);
+  std::fill_n(plan_host, table, 0);
+  int64_t next = 0;
+  for (int64_t b = 0; b < W; ++b) {
+    plan_host[2 * b] = int32_t(next);
+    plan_host[2 * b + 1] = int32_t(lists[b].size());
+    for (const int64_t d : lists[b]) {
+      int32_t* dst = plan_host + table + next * kItemInts;
+      std::copy_n(rec.data() + order[d % n] * kItemInts, kItemInts, dst);
+      dst[0] = int32_t(d / n);  // the KV head
+      ++next;
+    }
+  }
   return ok();
 }
 
@@ -626,8 +781,8 @@ extern "C" int kvc_batch_prefill_run(const kvc_prefill_schedule* sched, const in
   KVC_REQUIRE(sched, KVC_ERR_INVALID_ARG, "null schedule");
   const int Hq = sched->num_qo_heads, Hkv = sched->num_kv_heads;
   KVC_REQUIRE(Hkv > 0 && Hq % Hkv == 0 && sched->head_dim == kD && sched->page_size == kPage &&
-                  sched->tile_tokens == kTileRows / (Hq / Hkv) &&
-                  sched->plan_ints == int64_t(sched->num_items) * kItemInts,
+                  sched->tile_tokens == kTileRows / (Hq / Hkv) && sched->num_items >= 0 &&
+                  sched->plan_ints == plan_ints_for(sched->num_items, Hkv),
               KVC_ERR_INVALID_ARG, "schedule not produced by kvc_prefill_plan");
   if (sched->num_items == 0) return ok();
   KVC_REQUIRE(plan && q && key_cache && value_cache && out && indices, KVC_ERR_INVALID_ARG,
@@ -660,7 +815,9 @@ extern "C" int kvc_batch_prefill_run(const kvc_prefill_schedule* sched, const in
   a.num_blocks = num_blocks;
   a.indices = indices;
   a.num_indices = num_indices;
-  a.items = reinterpret_cast<const int4*>(plan);
+  const int64_t workgroups = plan_workgroups(sched->num_items, Hkv);
+  a.wg_units = reinterpret_cast<const int2*>(plan);
+  a.units = reinterpret_cast<const int4*>(plan + plan_table_ints(workgroups));
   a.num_kv_heads = Hkv;
   a.causal = sched->causal;
   a.scale_log2 = sm_scale * kLog2e;
@@ -669,10 +826,10 @@ extern "C" int kvc_batch_prefill_run(const kvc_prefill_schedule* sched, const in
   a.lse = lse;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (Hq / Hkv) {
-    case 1: launch<1>(a, sched->num_items, Hkv, s); break;
-    case 2: launch<2>(a, sched->num_items, Hkv, s); break;
-    case 4: launch<4>(a, sched->num_items, Hkv, s); break;
-    case 8: launch<8>(a, sched->num_items, Hkv, s); break;
+    case 1: launch<1>(a, int(workgroups), s); break;
+    case 2: launch<2>(a, int(workgroups), s); break;
+    case 4: launch<4>(a, int(workgroups), s); break;
+    case 8: launch<8>(a, int(workgroups), s); break;
     default: KVC_REQUIRE(false, KVC_ERR_UNSUPPORTED, "group must be 1, 2, 4 or 8");
   }
   KVC_LAUNCH_CHECK();

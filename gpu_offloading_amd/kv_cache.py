@@ -744,7 +744,7 @@ class PagedKVCache:
         o_val = o_pos + 2 * u
         o_dplan = (o_val + u + 3) // 4 * 4
         group = self.num_heads // self.num_kv_heads
-        pcap = pw._plan_capacity(np.asarray(clen), group) if C else 0
+        pcap = pw._plan_capacity(np.asarray(clen), group, self.num_kv_heads) if C else 0
         dcap = dw._plan_capacity(D) if D else 0
         while True:
             o_pplan = o_dplan + dcap

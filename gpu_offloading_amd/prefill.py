@@ -27,8 +27,10 @@ from . import _lib
 
 __all__ = ["BatchPrefillWithPagedKVCacheWrapper"]
 
-# Query rows (tokens x the GQA group) per work item of the prefill kernel.
+# Query rows (tokens x the GQA group) per work item of the prefill kernel,
+# and its most workgroups (one per CU; each runs a list of work items).
 _TILE_ROWS = 256
+_MAX_WORKGROUPS = 256
 
 
 def _fail(msg: str) -> None:
@@ -106,9 +108,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
         if num_kv_heads <= 0 or num_qo_heads % num_kv_heads:
             _fail("num_qo_heads must be a multiple of num_kv_heads")
         group = num_qo_heads // num_kv_heads
-        tile = _TILE_ROWS // group if group in (1, 2, 4, 8) else 1
         q_lens = np.diff(qo.astype(np.int64)) if batch > 0 else np.zeros(0, np.int64)
-        cap = int(np.sum((np.maximum(q_lens, 0) + tile - 1) // tile)) * 8 + 8
+        cap = self._plan_capacity(q_lens, group, num_kv_heads)
 
         sched = _lib.KvcPrefillSchedule()
         hs = torch.empty(cap, dtype=torch.int32, pin_memory=True)
@@ -133,12 +134,15 @@ class BatchPrefillWithPagedKVCacheWrapper:
 
     # ------------------------------------------------- in-package fast path
     @staticmethod
-    def _plan_capacity(q_lens: np.ndarray, group: int) -> int:
-        """int32 entries to reserve for the plan image (16-byte multiple)."""
+    def _plan_capacity(q_lens: np.ndarray, group: int, num_kv_heads: int) -> int:
+        """int32 entries to reserve for the plan image (16-byte multiple): the
+        workgroups' (first unit, units) table, padded to 4 entries, and one
+        8-entry record per (query tile, KV head)."""
         tile = _TILE_ROWS // group if group in (1, 2, 4, 8) else 1
         ql = np.maximum(np.asarray(q_lens, np.int64), 0)
-        cap = int(np.sum((ql + tile - 1) // tile)) * 8 + 8
-        return (cap + 3) // 4 * 4
+        units = int(np.sum((ql + tile - 1) // tile)) * max(int(num_kv_heads), 1)
+        table = (2 * min(_MAX_WORKGROUPS, units) + 3) // 4 * 4
+        return table + 8 * units + 8
 
     def _schedule_into(self, qo: np.ndarray, kv: np.ndarray, lpl: np.ndarray, batch: int,
                        num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int,

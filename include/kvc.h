@@ -244,9 +244,14 @@ int kvc_batch_decode_append_run(
  * natural-log log-sum-exp of the scaled logits.
  *
  * kvc_prefill_plan is host-only: it cuts every request's queries into tiles
- * of tile_tokens tokens (128 query rows = tile_tokens x group heads) and
- * orders them longest-first.  The plan image is num_items records of 8 int32:
- *   (request, first query, q_len, kv_len, qo_indptr[b], kv_indptr[b],
+ * of tile_tokens tokens (256 query rows = tile_tokens x group heads), makes
+ * one work unit per (tile, KV head) and deals the units to
+ * W = min(256, num_items * num_kv_heads) workgroups, one per CU, by list
+ * scheduling (longest tiles first, cost = key tiles + 2, workgroup w on XCD
+ * w % 8).  The plan image is the workgroups' table, W pairs
+ * (first unit, units) padded to a multiple of 4 int32, then
+ * num_items * num_kv_heads unit records of 8 int32 in workgroup order:
+ *   (KV head, first query, q_len, kv_len, qo_indptr[b], kv_indptr[b],
  *    64-key tiles to visit, pages)
  * If plan_capacity is too small it fills schedule->plan_ints and returns
  * KVC_ERR_WORKSPACE.  The caller copies the image (16-byte aligned) to the
@@ -260,10 +265,10 @@ typedef struct kvc_prefill_schedule {
   int32_t head_dim;
   int32_t page_size;
   int32_t causal;
-  int32_t tile_tokens;      /* query tokens per work item                  */
-  int32_t num_items;        /* work items per KV head                      */
+  int32_t tile_tokens;      /* query tokens per work unit                  */
+  int32_t num_items;        /* query tiles (work units per KV head)        */
   int32_t total_q;          /* qo_indptr[batch]                            */
-  int32_t max_key_tiles;    /* most 64-key tiles one item visits           */
+  int32_t max_key_tiles;    /* most 64-key tiles one unit visits           */
   int64_t plan_ints;        /* int32 entries of the plan image             */
 } kvc_prefill_schedule;
 

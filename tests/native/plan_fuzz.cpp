@@ -9,8 +9,10 @@
 //     single piece); workspace sized for max_partitions;
 //   decode, small-batch mode: one segment and one piece per request, at most
 //     16 pages each, no partials;
-//   prefill: every query of every request in exactly one work item, items
-//     ordered by descending key-tile count.
+//   prefill: every query of every request in exactly one work unit per KV
+//     head; the workgroup table covers the units once, no workgroup empty,
+//     and within each XCD's workgroups the loads (key tiles + 2 per unit)
+//     differ by at most one unit's cost.
 // Prints "ok <iterations>" and exits 0, or the first violation and exits 1.
 #include <algorithm>
 #include <cstdint>
@@ -94,22 +96,52 @@ int check_decode(const std::vector<int32_t>& indptr, const std::vector<int32_t>&
   return 0;
 }
 
-int check_prefill(const std::vector<int32_t>& qo, const std::vector<int32_t>& kv,
+int check_prefill(const std::vector<int32_t>& qo, const std::vector<int32_t>& kv, int hkv,
                   const kvc_prefill_schedule& s, const std::vector<int32_t>& img, int it) {
   const int B = s.batch;
-  std::vector<int64_t> covered(B, 0);
-  int prev_tiles = INT32_MAX;
-  for (int i = 0; i < s.num_items; ++i) {
-    const int32_t* r = img.data() + 8 * i;
-    CHECK(r[0] >= 0 && r[0] < B, "item request");
-    CHECK(r[2] == qo[r[0] + 1] - qo[r[0]] && r[4] == qo[r[0]] && r[5] == kv[r[0]],
-          "item offsets");
-    CHECK(r[1] >= 0 && r[1] < r[2] && r[1] % s.tile_tokens == 0, "item first query");
-    CHECK(r[6] <= prev_tiles, "longest first");
-    prev_tiles = r[6];
-    covered[r[0]] += std::min(r[1] + s.tile_tokens, r[2]) - r[1];
+  const int64_t units = int64_t(s.num_items) * hkv;
+  const int64_t W = std::min<int64_t>(256, units);
+  const int64_t table = (2 * W + 3) / 4 * 4;
+  CHECK(s.plan_ints == table + 8 * units, "prefill plan_ints");
+  // the workgroup table covers the unit records once, in order, none empty
+  int64_t next = 0;
+  std::vector<int64_t> load(W, 0);
+  int64_t max_cost = 0;
+  for (int64_t w = 0; w < W; ++w) {
+    CHECK(img[2 * w] == next && img[2 * w + 1] >= 1, "workgroup table");
+    for (int64_t u = next; u < next + img[2 * w + 1]; ++u) {
+      const int64_t c = img[table + 8 * u + 6] + 2;
+      load[w] += c;
+      max_cost = std::max(max_cost, c);
+    }
+    next += img[2 * w + 1];
   }
-  for (int b = 0; b < B; ++b) CHECK(covered[b] == qo[b + 1] - qo[b], "queries covered once");
+  CHECK(next == units, "every unit in one workgroup");
+  // list scheduling: within each XCD's workgroups, loads within one unit's cost
+  const int groups = W % 8 == 0 ? 8 : 1;
+  for (int x = 0; x < groups; ++x) {
+    int64_t lo = INT64_MAX, hi = 0;
+    for (int64_t w = x; w < W; w += groups) lo = std::min(lo, load[w]), hi = std::max(hi, load[w]);
+    CHECK(hi - lo <= max_cost, "workgroup balance");
+  }
+  // every query of every request in exactly one unit per KV head
+  std::vector<int> req_of_q(qo.empty() ? 0 : size_t(qo[B]) + 1, -1);
+  for (int b = 0; b < B; ++b)
+    if (qo[b + 1] > qo[b]) req_of_q[size_t(qo[b])] = b;
+  std::vector<int64_t> covered(size_t(B) * hkv, 0);
+  for (int64_t u = 0; u < units; ++u) {
+    const int32_t* r = img.data() + table + 8 * u;
+    CHECK(r[0] >= 0 && r[0] < hkv, "unit head");
+    CHECK(r[4] >= 0 && r[4] < int64_t(req_of_q.size()) && req_of_q[size_t(r[4])] >= 0,
+          "unit request");
+    const int b = req_of_q[size_t(r[4])];
+    CHECK(r[2] == qo[b + 1] - qo[b] && r[5] == kv[b], "unit offsets");
+    CHECK(r[1] >= 0 && r[1] < r[2] && r[1] % s.tile_tokens == 0, "unit first query");
+    covered[size_t(b) * hkv + r[0]] += std::min(r[1] + s.tile_tokens, r[2]) - r[1];
+  }
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < hkv; ++h)
+      CHECK(covered[size_t(b) * hkv + h] == qo[b + 1] - qo[b], "queries covered once per head");
   return 0;
 }
 
@@ -165,7 +197,7 @@ int main(int argc, char** argv) {
                             causal, &ps, pimg.data(), int64_t(pimg.size()));
     }
     CHECK(st == KVC_OK, "prefill plan of a valid batch");
-    if (check_prefill(qo, indptr, ps, pimg, it)) return 1;
+    if (check_prefill(qo, indptr, hkv, ps, pimg, it)) return 1;
   }
   std::printf("ok %d\n", iters);
   return 0;

@@ -367,6 +367,8 @@ def test_entry_points_validate_before_touching_the_gpu(lib):
 
 
 def _prefill_plan(lib, q_lens, kv_lens, hq=32, hkv=8, causal=1, cap=None):
+    """kvc_prefill_plan; returns (status, schedule, workgroup table [W, 2],
+    unit records [U, 8], qo_indptr, kv_indptr)."""
     qo = np.zeros(len(q_lens) + 1, np.int32)
     np.cumsum(q_lens, out=qo[1:])
     pages = [(k + 15) // 16 for k in kv_lens]
@@ -378,19 +380,29 @@ def _prefill_plan(lib, q_lens, kv_lens, hq=32, hkv=8, causal=1, cap=None):
     st = lib.kvc_prefill_plan(qo.ctypes.data, kvi.ctypes.data, lpl.ctypes.data, len(q_lens),
                               hq, hkv, 128, 16, causal, ctypes.byref(sched), img.ctypes.data,
                               img.size)
-    return st, sched, img[:max(sched.plan_ints, 0)].reshape(-1, 8), qo, kvi
+    w = min(256, sched.num_items * hkv)
+    table = (2 * w + 3) // 4 * 4
+    if st != 0:
+        return st, sched, None, None, qo, kvi
+    assert sched.plan_ints == table + 8 * sched.num_items * hkv
+    return st, sched, img[:2 * w].reshape(-1, 2), img[table:sched.plan_ints].reshape(-1, 8), qo, kvi
 
 
-def test_prefill_plan_tiles_every_query_once_longest_first(lib):
+def test_prefill_plan_tiles_every_query_once_per_head(lib):
     q_lens, kv_lens = [1, 17, 40, 64, 130, 0, 33], [1, 40, 40, 300, 130, 12, 1000]
-    st, sched, rec, qo, kvi = _prefill_plan(lib, q_lens, kv_lens)
+    hkv = 8
+    st, sched, wg, rec, qo, kvi = _prefill_plan(lib, q_lens, kv_lens, hkv=hkv)
     assert st == 0, lib.kvc_last_error()
     T = sched.tile_tokens                                         # 256 query rows / group 4
     assert T == 64 and sched.total_q == sum(q_lens)
-    assert (np.diff(rec[:, 6]) <= 0).all()                        # longest first
+    n = sched.num_items
+    assert n == sum((q + T - 1) // T for q in q_lens) and len(rec) == n * hkv
+    # the table covers the records once, in order
+    assert wg[0, 0] == 0 and (wg[1:, 0] == np.cumsum(wg[:-1, 1])).all() and wg[:, 1].sum() == len(rec)
     for b, (ql, kl) in enumerate(zip(q_lens, kv_lens)):
-        mine = rec[rec[:, 0] == b]
-        assert sorted(mine[:, 1].tolist()) == list(range(0, ql, T))
+        mine = rec[(rec[:, 4] == qo[b]) & (rec[:, 5] == kvi[b]) & (rec[:, 2] == ql)]
+        for h in range(hkv):
+            assert sorted(mine[mine[:, 0] == h][:, 1].tolist()) == list(range(0, ql, T))
         for r in mine:
             assert (r[2], r[3], r[4], r[5], r[7]) == (ql, kl, qo[b], kvi[b], kvi[b + 1] - kvi[b])
             last = min(r[1] + T, ql) - 1
@@ -398,17 +410,36 @@ def test_prefill_plan_tiles_every_query_once_longest_first(lib):
             assert r[6] == (keys + 63) // 64
     assert sched.max_key_tiles == rec[:, 6].max()
     # non-causal: every tile visits the whole cache
-    st, sched, rec, _, _ = _prefill_plan(lib, q_lens, kv_lens, causal=0)
+    st, sched, wg, rec, _, _ = _prefill_plan(lib, q_lens, kv_lens, causal=0)
     assert st == 0
     assert all(r[6] == (r[3] + 63) // 64 for r in rec)
     # group 8 packs 32 tokens x 8 heads per tile
-    st, sched, rec, _, _ = _prefill_plan(lib, [100], [100], hq=16, hkv=2)
-    assert st == 0 and sched.tile_tokens == 32 and sched.num_items == 4
+    st, sched, wg, rec, _, _ = _prefill_plan(lib, [100], [100], hq=16, hkv=2)
+    assert st == 0 and sched.tile_tokens == 32 and sched.num_items == 4 and len(wg) == 8
+
+
+def test_prefill_plan_balances_the_workgroups(lib):
+    """256 persistent workgroups, unit costs key tiles + 2: within each XCD's
+    32 workgroups the loads differ by at most one unit's cost (list
+    scheduling), and the workgroups of one XCD run one request's units."""
+    q_lens, kv_lens = [2048] * 8, [4096] * 8
+    st, sched, wg, rec, qo, _ = _prefill_plan(lib, q_lens, kv_lens)
+    assert st == 0 and len(wg) == 256 and len(rec) == 256 * 8
+    cost = rec[:, 6] + 2
+    loads = np.array([cost[f:f + c].sum() for f, c in wg])
+    for x in range(8):
+        mine = loads[x::8]
+        assert mine.max() - mine.min() <= cost.max(), (x, mine.min(), mine.max())
+        reqs = {int(r[4]) for f, c in wg[x::8] for r in rec[f:f + c]}
+        assert reqs == {int(qo[x])}, (x, reqs)
+    # fewer units than workgroups: one unit each
+    st, sched, wg, rec, _, _ = _prefill_plan(lib, [100], [300])
+    assert st == 0 and len(wg) == len(rec) == 2 * 8 and (wg[:, 1] == 1).all()
 
 
 def test_prefill_plan_reports_capacity_and_rejects_bad_input(lib):
-    st, sched, _, _, _ = _prefill_plan(lib, [100, 40], [100, 40], cap=8)
-    assert st == 4 and sched.plan_ints == 8 * (2 + 1)
+    st, sched, _, _, _, _ = _prefill_plan(lib, [100, 40], [100, 40], cap=8)
+    assert st == 4 and sched.plan_ints == 48 + 8 * 3 * 8          # table + 24 unit records
     assert b"plan buffer too small" in lib.kvc_last_error()
     st, *_ = _prefill_plan(lib, [10], [10], hq=24, hkv=8)
     assert st == 2                                                 # group 3
@@ -421,7 +452,7 @@ def test_prefill_plan_reports_capacity_and_rejects_bad_input(lib):
                                 16, 1, ctypes.byref(sched), img.ctypes.data, 64) == 1
     assert b"non-decreasing" in lib.kvc_last_error()
     # zero items: the run is a no-op even with null pointers
-    st, sched, _, _, _ = _prefill_plan(lib, [0], [16])
+    st, sched, _, _, _, _ = _prefill_plan(lib, [0], [16])
     assert st == 0 and sched.num_items == 0
     assert lib.kvc_batch_prefill_run(ctypes.byref(sched), None, None, 4096, None, None, 16384,
                                      1024, 1, None, 0, 0.1, None, 4096, None, None) == 0

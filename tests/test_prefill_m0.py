@@ -3,9 +3,11 @@ here with hipcc): its direct-to-LDS loads (global_load_lds_dwordx4, buffer_load
 ... lds) take their LDS address from M0, which the inline assembly writes and
 cannot declare clobbered (hipcc reserves M0).  So nothing the compiler
 generates may use M0: every instruction naming M0 is one of the kernel's own
-`s_mov_b32 m0, sN`, each directly followed by a direct-to-LDS load, every such
-load directly preceded by one, and no instruction that reads M0 implicitly
-(relative moves, messages, interpolation, GWS, append/consume) appears."""
+M0 writes -- `s_mov_b32 m0, sN` or, between the four loads of one page,
+`s_add_u32 m0, m0, 0x400` right after a load -- each directly followed by a
+direct-to-LDS load, every such load directly preceded by one, and no
+instruction that reads M0 implicitly (relative moves, messages,
+interpolation, GWS, append/consume) appears."""
 import os
 import re
 import subprocess
@@ -39,13 +41,18 @@ def test_only_the_direct_lds_loads_use_m0(tmp_path):
                     "-o", str(out)], check=True, capture_output=True)
     ins = list(_instructions(out.read_text()))
     assert ins, "empty assembly"
+    set_m0 = re.compile(r"^s_mov_b32 m0, s\d+$")
+    step_m0 = re.compile(r"^s_add_u32 m0, m0, 0x400$")
     n_dma = 0
     for i, code in enumerate(ins):
         assert not IMPLICIT_M0.match(code), code
         if LDS_DMA.match(code):
             n_dma += 1
-            assert i > 0 and re.match(r"^s_mov_b32 m0, s\d+$", ins[i - 1]), (ins[i - 1], code)
+            assert i > 0 and (set_m0.match(ins[i - 1]) or step_m0.match(ins[i - 1])), \
+                (ins[i - 1], code)
         if re.search(r"\bm0\b", code):
-            assert re.match(r"^s_mov_b32 m0, s\d+$", code), code
+            assert set_m0.match(code) or step_m0.match(code), code
+            if step_m0.match(code):
+                assert i > 0 and LDS_DMA.match(ins[i - 1]), (ins[i - 1], code)
             assert i + 1 < len(ins) and LDS_DMA.match(ins[i + 1]), (code, ins[i + 1:i + 2])
     assert n_dma > 0
