@@ -1,6 +1,10 @@
 """GPU parity of paged-KV prefill attention (continuation prefill, MFMA)
 against the fp32 CPU oracle: max-abs-error <= 2e-2 and mean-abs-error <= 2e-3
-on the bf16 output; lse within 2e-3."""
+on the bf16 output; lse within LSE_TOL.  The kernel sums the row's
+probabilities as rounded to bf16 for the P.V product (round to nearest, 8
+significant bits: relative error <= 2^-8 per term), so its l is within a
+factor 1 +- 2^-8 of the exact sum and lse = m + ln l within ln(1 + 2^-8) =
+0.0039 of it, plus fp32 rounding."""
 import numpy as np
 import pytest
 import torch
@@ -14,6 +18,7 @@ from oracle import kv_oracle as orc
 pytestmark = pytest.mark.gpu
 
 WS = 16 * 1024 * 1024
+LSE_TOL = 4e-3
 
 
 def _case(q_lens, kv_lens, hq, hkv, seed, d=128, extra_pages=8, device=None):
@@ -52,7 +57,7 @@ def _check(gpu, q_lens, kv_lens, hq, hkv, seed, causal=True):
     got_lse = lse.cpu().numpy()
     fin = np.isfinite(ref_lse)
     assert np.array_equal(np.isneginf(got_lse), ~fin)
-    assert np.abs(got_lse[fin] - ref_lse[fin]).max() < 2e-3
+    assert np.abs(got_lse[fin] - ref_lse[fin]).max() < LSE_TOL
     return w
 
 
@@ -93,7 +98,7 @@ def test_prefill_nan_past_the_end(gpu, q_len, kv_len):
     ref, ref_lse = orc.paged_prefill(u16(q), u16(kc), u16(vc), qo, kvi, idx, lpl)
     assert torch.isfinite(out).all()
     assert_attn_close(out.float().cpu().numpy(), ref)
-    assert np.abs(lse.cpu().numpy() - ref_lse).max() < 2e-3
+    assert np.abs(lse.cpu().numpy() - ref_lse).max() < LSE_TOL
 
 
 def test_prefill_missing_pages_are_hidden(gpu):
@@ -121,8 +126,50 @@ def test_prefill_missing_pages_are_hidden(gpu):
     got_lse = lse.cpu().numpy()
     fin = np.isfinite(ref_lse)
     assert np.array_equal(np.isneginf(got_lse), ~fin)
-    assert np.abs(got_lse[fin] - ref_lse[fin]).max() < 2e-3
+    assert np.abs(got_lse[fin] - ref_lse[fin]).max() < LSE_TOL
     assert (out[qo[3]:qo[4]] == 0).all()
+
+
+def test_prefill_workgroups_chain_many_units(gpu):
+    """More (query tile, KV head) units than workgroups, so each persistent
+    workgroup runs a list of them: ragged chunks, chunks longer than their
+    cache (units that see no key sit between units that do, so a unit after
+    them starts cold), missing pages and NaN past the end of partial pages.
+    The plan image is read back to show that those chains occur."""
+    rng = np.random.default_rng(61)
+    q_lens = rng.integers(1, 300, 30).tolist()
+    kv_lens = [q + int(rng.integers(0, 500)) for q in q_lens]
+    for b in (3, 11, 19):                         # first units see no key
+        kv_lens[b] = int(rng.integers(1, max(2, q_lens[b] // 3)))
+    q_lens[25], kv_lens[25] = 150, 0              # a request with no pages
+    q, kc, vc, qo, kvi, idx, lpl = _case(q_lens, kv_lens, 32, 8, 62, device=gpu)
+    idx = idx.copy()
+    for b in (4, 8, 13):                          # a missing page mid-request
+        if kvi[b + 1] - kvi[b] > 3:
+            idx[kvi[b] + 2] = -1
+    for b in range(len(q_lens)):                  # NaN bits past kv_len
+        if kv_lens[b] % 16:
+            last = int(idx[kvi[b + 1] - 1])
+            if last >= 0:
+                kc[last, kv_lens[b] % 16:] = float("nan")
+                vc[last, kv_lens[b] % 16:] = float("nan")
+    (out, lse), w = _run(gpu, q, kc, vc, qo, kvi, idx, lpl, 32, 8)
+    plan = w._plan_dev.cpu().numpy()
+    units = w.schedule.num_items * 8
+    wgs = min(256, units)
+    table = plan[:2 * wgs].reshape(-1, 2)
+    rec = plan[(2 * wgs + 3) // 4 * 4:][:units * 8].reshape(-1, 8)
+    assert units > 256 and table[:, 1].max() >= 2
+    cold = sum(1 for f, c in table for u in range(f + 1, f + c)
+               if rec[u - 1, 6] == 0 and rec[u, 6] > 0)
+    assert cold > 0                               # a unit after one with no key tiles
+    ref, ref_lse = orc.paged_prefill(u16(q), u16(kc), u16(vc), qo, kvi, idx, lpl)
+    assert torch.isfinite(out).all()
+    assert_attn_close(out.float().cpu().numpy(), ref)
+    got_lse = lse.cpu().numpy()
+    fin = np.isfinite(ref_lse)
+    assert np.array_equal(np.isneginf(got_lse), ~fin)
+    assert np.abs(got_lse[fin] - ref_lse[fin]).max() < LSE_TOL
 
 
 def test_prefill_long_continuation(gpu):
@@ -141,7 +188,7 @@ def test_prefill_one_token_chunks_match_decode_kernel(gpu):
             num_qo_heads=32, num_kv_heads=8, head_dim=128, page_size=16)
     dout, dlse = wd.run(q, (kc.to(gpu), vc.to(gpu)), return_lse=True)
     assert_attn_close(out.float().cpu().numpy(), dout.float().cpu().numpy())
-    assert (lse - dlse).abs().max().item() < 2e-3
+    assert (lse - dlse).abs().max().item() < LSE_TOL
 
 
 def test_prefill_strided_q_and_out(gpu):
@@ -199,7 +246,7 @@ def test_cache_continuation_prefill_flow(gpu):
         ref, ref_lse = orc.paged_prefill(u16(q), u16(cache.k_cache[0]), u16(cache.v_cache[0]),
                                          qo, kvi, idx, lpl, causal=True)
         assert_attn_close(out.float().cpu().numpy(), ref)
-        assert np.abs(lse.cpu().numpy() - ref_lse).max() < 2e-3
+        assert np.abs(lse.cpu().numpy() - ref_lse).max() < LSE_TOL
 
 
 @pytest.mark.parametrize("kv_len", [2048, 4096])
