@@ -711,7 +711,8 @@ extern "C" int kvc_prefill_plan(const int32_t* qo_indptr_host, const int32_t* kv
     }
   }
   const int64_t n = int64_t(rec.size()) / kItemInts;
-  KVC_REQUIRE(n < (int64_t(1) << 31), KVC_ERR_INVALID_ARG, "too many query tiles");
+  KVC_REQUIRE(n * num_kv_heads < (int64_t(1) << 30), KVC_ERR_INVALID_ARG,
+              "too many (query tile, KV head) units");
   sched->batch = batch;
   sched->num_qo_heads = num_qo_heads;
   sched->num_kv_heads = num_kv_heads;
