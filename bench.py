@@ -710,14 +710,19 @@ def run_offload(torch, seed, steps=3):
     snap = cache.k_cache[5][cache.block_table[0, :256].long()].clone()
     torch.cuda.synchronize()
     # One untimed preemption and resume of the same request first: the first
-    # copies over the host link in a process were measured at ~34 GB/s
-    # against 57 GB/s for every later one (one-time, not a property of the
-    # swap path), and would otherwise set the timed figure.
+    # copies through a newly pinned host buffer were measured at 25-40 GB/s
+    # against 55-57 GB/s for every later one through the same buffer (a
+    # one-time cost per buffer, not a property of the swap path), and would
+    # otherwise set the timed figure.
     hw = pre.preempt(0, key="warm")
     cache.synchronize_swaps()
     pre.resume("warm", slot=2)
     cache.synchronize_swaps()
     first = (hw.num_bytes / hw.out_seconds() / 1e9, hw.num_bytes / hw.in_seconds() / 1e9)
+    # Release the warm-up's host image, so that the timed swap-out reuses it
+    # from torch's pinned-memory cache as an engine that frees resumed images
+    # would: a freshly pinned buffer's first copies run at 25-40 GB/s.
+    del hw
     h = pre.preempt(2, key="r0")
     cache.synchronize_swaps()
     t_out = h.out_seconds()
