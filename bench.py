@@ -630,7 +630,7 @@ def run_offload(torch, seed, steps=3):
     the same step all-resident, and the host-link rate of the staging.
     (b) Swap preemption, Mixtral-shaped (32 layers, Hkv 8, D 128, bf16): one
     4096-token request swapped out and back in."""
-    from gpu_offloading_amd import ops
+    from gpu_offloading_amd import hostmem, ops
     from gpu_offloading_amd.kv_cache import PagedKVCache
     from gpu_offloading_amd.offload import KVOffloadPipeline, PagedOffloadKV, SwapPreemption
 
@@ -686,15 +686,20 @@ def run_offload(torch, seed, steps=3):
         r = {"kv_offload_ratio": ratio, "step_ms": wall * 1e3}
         if pipe:
             cs = pipe.copy_seconds()
+            # The write-back (D2H) span also holds the gather of the prefill
+            # blocks on the D2H stream, beside the compute: a stream span,
+            # not a link rate.
             r.update({"h2d_GB_per_step": pipe.h2d_bytes / steps / 1e9,
                       "h2d_GBps": pipe.h2d_bytes / cs["h2d"] / 1e9,
-                      "d2h_GBps": pipe.d2h_bytes / cs["d2h"] / 1e9 if cs["d2h"] else None,
+                      "d2h_GB_per_step": pipe.d2h_bytes / steps / 1e9,
+                      "d2h_stream_ms_per_step": cs["d2h"] / steps * 1e3,
                       "link_bound_step_ms": cs["h2d"] / steps * 1e3})
         res[f"layer_offload_ratio_{ratio}"] = r
         log(f"offload ratio {ratio}: step {wall * 1e3:.2f} ms" +
             (f", H2D {r['h2d_GB_per_step']:.2f} GB/step at {r['h2d_GBps']:.1f} GB/s "
              f"(copy-stream time {r['link_bound_step_ms']:.2f} ms/step), "
-             f"D2H {r['d2h_GBps']:.1f} GB/s" if pipe else ""))
+             f"write-back {r['d2h_GB_per_step'] * 1e3:.0f} MB/step in "
+             f"{r['d2h_stream_ms_per_step']:.2f} ms of D2H-stream time" if pipe else ""))
         del kv, pipe, ks, qs, out
         torch.cuda.empty_cache()
 
@@ -708,22 +713,19 @@ def run_offload(torch, seed, steps=3):
     pre = SwapPreemption(cache)
     cache.reserve_swap()
     snap = cache.k_cache[5][cache.block_table[0, :256].long()].clone()
+    # The host image comes from a pool, as an engine would keep one: the
+    # first copies through a newly pinned buffer run at ~34 GB/s against
+    # 55-57 GB/s for every later one through it.
+    image = hostmem.pinned_empty(32 * 256 * 2 * ops.block_bytes(cache.k_cache[0]))
     torch.cuda.synchronize()
-    # One untimed preemption and resume of the same request first: the first
-    # copies through a newly pinned host buffer were measured at 25-40 GB/s
-    # against 55-57 GB/s for every later one through the same buffer (a
-    # one-time cost per buffer, not a property of the swap path), and would
-    # otherwise set the timed figure.
-    hw = pre.preempt(0, key="warm")
+    # One untimed preemption and resume of the same request first (through
+    # the same buffer), whose rates are reported beside the timed ones.
+    hw = pre.preempt(0, key="warm", host=image)
     cache.synchronize_swaps()
     pre.resume("warm", slot=2)
     cache.synchronize_swaps()
     first = (hw.num_bytes / hw.out_seconds() / 1e9, hw.num_bytes / hw.in_seconds() / 1e9)
-    # Release the warm-up's host image, so that the timed swap-out reuses it
-    # from torch's pinned-memory cache as an engine that frees resumed images
-    # would: a freshly pinned buffer's first copies run at 25-40 GB/s.
-    del hw
-    h = pre.preempt(2, key="r0")
+    h = pre.preempt(2, key="r0", host=image)
     cache.synchronize_swaps()
     t_out = h.out_seconds()
     pre.resume("r0", slot=1)

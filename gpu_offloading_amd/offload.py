@@ -75,10 +75,15 @@ class SwapPreemption:
             self.cache.k_cache[0][0].numel() * self.cache.k_cache[0].element_size()
         return self.host_bytes_in_use + need <= self.host_budget_bytes
 
-    def preempt(self, slot: int, key) -> SwapHandle:
+    def preempt(self, slot: int, key, host=None) -> SwapHandle:
+        """Swap ``slot`` out under ``key``.  ``host``: an optional pinned host
+        buffer to hold the image (``PagedKVCache.swap_out``); an engine that
+        keeps a pool of them avoids pinning a new buffer per preemption, and
+        the first copies through a newly pinned buffer run well below the
+        link rate."""
         if key in self._swapped:
             raise RuntimeError(f"request {key!r} is already swapped out")
-        handle = self.cache.swap_out([slot])
+        handle = self.cache.swap_out([slot], host=host)
         self._swapped[key] = handle
         self.swaps_out += 1
         return handle
