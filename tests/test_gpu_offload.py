@@ -116,9 +116,9 @@ def test_offload_pipeline_matches_resident_layout(gpu, ratio, mode):
 
 def test_swap_preemption_resumes_bit_identically(gpu):
     """Four sequences decode for 8 steps; in the tight pool the scheduler
-    preempts the last one at step 2 (swap) and resumes it at step 5 in
-    another slot.  The reference pool pauses it in place.  Every decode
-    output matches bit for bit."""
+    preempts the last one at step 2 (swap, into a caller-owned pinned image)
+    and resumes it at step 5 in another slot.  The reference pool pauses it
+    in place.  Every decode output matches bit for bit."""
     L, Hkv, Hq = 2, 8, 32
     kw = dict(num_qo_heads=Hq, device=gpu, workspace_bytes=1 << 24, staging_bytes=1 << 22)
     tight = PagedKVCache(L, Hkv, 128, max_seqs=6, max_seq_len=640, kv_page_budget=110,
@@ -145,9 +145,14 @@ def test_swap_preemption_resumes_bit_identically(gpu):
     pre = SwapPreemption(tight)
     where = {0: 0, 1: 1, 2: 2, 3: 3}   # request -> slot in the tight cache
     used_before = tight.pages_in_use
+    # the image goes into a caller-owned pinned buffer (an engine's pool),
+    # larger than needed
+    need = L * ((lens[3] + 2 + 15) // 16) * 2 * tight.k_cache[0][0].numel() * 2
+    pool = torch.empty(2 * need, dtype=torch.uint8, pin_memory=True)
     for step in range(8):
         if step == 2:
-            pre.preempt(where.pop(3), key=3)
+            h = pre.preempt(where.pop(3), key=3, host=pool)
+            assert h.host.data_ptr() == pool.data_ptr()
             tight.synchronize_swaps()
             assert tight.pages_in_use == used_before - (lens[3] + 15) // 16
         if step == 5:
