@@ -242,11 +242,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
     return RawIds{a.indices[min(U.page_off + tile * 4 + (lane & 3), last_index)]};
   };
   // Byte offset of this wave's page of a tile, at the unit's head (the host
-  // keeps a block stride under 4 GiB), and the tile's present pages: bit u of `ok` says page u is
-  // real (inside the request and the cache); the others read block 0 and
-  // are masked.  Pages [0, pages_here) of the item exist in the request and
-  // the index array; a present page also needs an id in [0, num_blocks).  The
-  // four tests run on lanes 0..3 at once and one ballot collects them.
+  // keeps a block stride under 4 GiB), and the tile's present pages: bit u
+  // of `ok` says page u is real (inside the request and the cache); the
+  // others read block 0 and are masked.  Pages [0, pages_here) of the unit
+  // exist in the request and the index array; a present page also needs an
+  // id in [0, num_blocks).  The four tests run on lanes 0..3 at once and
+  // one ballot collects them.
   const uint32_t blk32 = uint32_t(a.block_stride * 2);
   struct Pages { uint64_t off; int ok; };
   auto resolve = [&](const Unit& U, const RawIds& t, int tile) __attribute__((always_inline)) {
@@ -269,8 +270,6 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
   auto lds_addr = [](const void* p) __attribute__((always_inline)) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t*)p));
   };
-  // K: one instruction of a wave fills 1 KB of LDS (keys 4i .. 4i+3 of the
-  // wave's page): one block address per wave and tile.
   // A wave-uniform 64-bit value as an SGPR pair (the page offsets are
   // uniform, but the compiler may keep them in VGPRs).
   auto sgpr64 = [](uint64_t v) __attribute__((always_inline)) {
@@ -278,6 +277,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
     const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
     return (uint64_t(hi) << 32) | lo;
   };
+  // K: one instruction of a wave fills 1 KB of LDS (keys 4i .. 4i+3 of the
+  // wave's page); the page's four come from one block address, with M0
+  // stepped by 1 KB between them.
   auto dma_k = [&](KTile& buf, const Pages& p) __attribute__((always_inline)) {
     const uint64_t blk = sgpr64(reinterpret_cast<uint64_t>(kbase + p.off));
     asm volatile("s_mov_b32 m0, %0\n\t"
