@@ -62,6 +62,7 @@ constexpr int kKeys = 64;                     // keys per tile
 constexpr int kPage = 16;
 constexpr int kD = 128;
 constexpr int kKRow = kD * 2;                // bytes per K or V row in LDS (unpadded)
+constexpr int kORow = kKRow + 16;            // bytes per staged output row
 constexpr int kItemInts = 8;
 constexpr float kRescaleLog2 = 8.f;           // lazy-rescale threshold (base 2)
 // Word 3 of a raw buffer resource (32-bit data, no swizzle): loads past
@@ -107,6 +108,8 @@ struct alignas(16) VTile { uint8_t b[kKeys * kKRow]; };
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Two floats as a bf16 pair (v_cvt_pk_bf16_f32: round to nearest even).
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
@@ -154,8 +157,20 @@ struct Unit { int h, tok0, q_len, kv_len, q_off, page_off, ntiles, npages; };
 template <int G>
 __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int kTokPerWave = kWaveRows / G;
-  __shared__ KTile ktiles[2];
-  __shared__ VTile vtiles[2];
+  // One LDS object, so that the K/V tiles sit in its first 64 KB (operand
+  // reads then address them with immediate offsets) and the output staging
+  // after them: each wave's finished rows on their way out, 32 rows of
+  // 256 B padded to kORow (a row's 16 pieces written by one instruction then
+  // spread over the banks, and every lane address is a base plus an
+  // immediate).
+  struct Lds {
+    KTile k[2];
+    VTile v[2];
+    uint8_t ostage[8][kWaveRows * kORow];
+  };
+  __shared__ Lds lds;
+  KTile (&ktiles)[2] = lds.k;
+  VTile (&vtiles)[2] = lds.v;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
   const int team = wave >> 2;
@@ -476,25 +491,60 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
   };
 
   // The unit's output rows: O / l in bf16 and, when asked, the natural-log
-  // log-sum-exp; then the running state starts over for the next unit.
+  // log-sum-exp; then the running state starts over for the next unit.  The
+  // rows go out through this wave's LDS staging: each lane holds 8-byte
+  // pieces of one row, which as stores would touch 32 rows per instruction;
+  // read back, lane L of store t holds 16 bytes of row 4t + L/16, so a store
+  // writes four whole rows (one token's four heads at G = 4: 1 KB in a run).
+  // The stores are non-temporal: the output is not read again here, and
+  // leaving it out of the caches keeps the K/V tiles the other query tiles
+  // of a request re-read there.
   auto finish_unit = [&]() __attribute__((always_inline)) {
     const float l_run = l_half + __shfl_xor(l_half, 32);
-    if (row_ok) {
-      // O^T column r = this row; entry (db, 4i+j) = head dim 32db + 8i + 4half + j.
-      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-      uint16_t* dst = a.out + int64_t(cu.q_off + tok) * a.out_stride + int64_t(hq) * kD + 4 * half;
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    uint8_t* stg = lds.ostage[wave];
+    // O^T column r = this row; entry (db, 4i+j) = head dim 32db + 8i + 4half + j,
+    // so (db, i) is the row's 16-byte chunk 4db + i and half its 8-byte half.
+    uint8_t* wr = stg + r * kORow + 8 * half;
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4; ++db) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          *reinterpret_cast<uint2*>(dst + 32 * db + 8 * i) =
-              make_uint2(pack_bf16(o[db][4 * i] * inv, o[db][4 * i + 1] * inv),
-                         pack_bf16(o[db][4 * i + 2] * inv, o[db][4 * i + 3] * inv));
-        }
-      if (a.lse && half == 0)
-        a.lse[int64_t(cu.q_off + tok) * Hq + hq] =
-            l_run > 0.f ? (m_run + fast_log2(l_run)) * kLn2 : -INFINITY;
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<uint2*>(wr + 16 * (4 * db + i)) =
+            make_uint2(pack_bf16(o[db][4 * i] * inv, o[db][4 * i + 1] * inv),
+                       pack_bf16(o[db][4 * i + 2] * inv, o[db][4 * i + 3] * inv));
+      __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // Row 4t + q (q = L/16 < 4) is token (4t + q) / G of the wave, head
+    // (4t + q) % G: for G <= 4 that is token t (4/G) + q/G, head q % G; for
+    // G >= 4 token 4t/G, head 4t % G + q.  So the lane's part of the address
+    // is set once and the store's part is uniform.
+    const int c = lane & 15;
+    const int q = lane >> 4;
+    const int wave_tok = cu.tok0 + wave * kTokPerWave;
+    const int toks_left = cu.q_len - wave_tok;
+    const int lane_tok = G <= 4 ? q / G : 0;
+    const int lane_head = G <= 4 ? q % G : q;
+    uint16_t* obase = a.out + int64_t(cu.q_off + wave_tok + lane_tok) * a.out_stride +
+                      int64_t(cu.h * G + lane_head) * kD + 8 * c;
+    const uint8_t* rd = stg + q * kORow + 16 * c;
+#pragma unroll
+    for (int t = 0; t < kWaveRows / 4; ++t) {
+      const int t_tok = G <= 4 ? t * (4 / G) : 4 * t / G;
+      const int t_head = G <= 4 ? 0 : 4 * t % G;
+      const uint4 v = *reinterpret_cast<const uint4*>(rd + 4 * t * kORow);
+      if (t_tok + lane_tok < toks_left)
+        __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w},
+                                    reinterpret_cast<u32x4*>(obase + int64_t(t_tok) * a.out_stride +
+                                                             t_head * kD));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (row_ok && a.lse && half == 0)
+      a.lse[int64_t(cu.q_off + tok) * Hq + hq] =
+          l_run > 0.f ? (m_run + fast_log2(l_run)) * kLn2 : -INFINITY;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -803,11 +853,11 @@ extern "C" int kvc_batch_prefill_run(const kvc_prefill_schedule* sched, const in
   KVC_REQUIRE(sm_scale > 0.f && std::isfinite(sm_scale), KVC_ERR_INVALID_ARG,
               "sm_scale must be positive and finite");
   KVC_REQUIRE(aligned(q, 16) && aligned(key_cache, 16) && aligned(value_cache, 16) &&
-                  aligned(out, 8) && aligned(plan, 16) && q_token_stride % 8 == 0 &&
-                  out_token_stride % 4 == 0 && cache_block_stride % 8 == 0 &&
+                  aligned(out, 16) && aligned(plan, 16) && q_token_stride % 8 == 0 &&
+                  out_token_stride % 8 == 0 && cache_block_stride % 8 == 0 &&
                   cache_token_stride % 8 == 0,
-              KVC_ERR_ALIGNMENT, "q/cache/plan must be 16-byte aligned (out 8-byte) with "
-                                 "matching strides");
+              KVC_ERR_ALIGNMENT, "q/out/cache/plan must be 16-byte aligned with matching "
+                                 "strides");
   PrefillArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.q_stride = q_token_stride;

@@ -280,8 +280,10 @@ int kvc_prefill_plan(const int32_t* qo_indptr_host, const int32_t* kv_indptr_hos
                      int64_t plan_capacity);
 
 /* q/out: [total_q][num_qo_heads][head_dim] with a token stride (elements).
- * The cache's block stride must stay under 4 GiB (2^31 elements) and a
- * block's 16 tokens under 2 GiB: KVC_ERR_INVALID_ARG otherwise. */
+ * q, out, the caches and the plan 16-byte aligned, every stride a multiple
+ * of 8 elements (KVC_ERR_ALIGNMENT otherwise).  The cache's block stride
+ * must stay under 4 GiB (2^31 elements) and a block's 16 tokens under
+ * 2 GiB: KVC_ERR_INVALID_ARG otherwise. */
 int kvc_batch_prefill_run(
     const kvc_prefill_schedule* schedule, const int32_t* plan,
     const void* q, int64_t q_token_stride,
