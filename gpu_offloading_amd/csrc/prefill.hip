@@ -36,7 +36,9 @@
 // ds_read_b64_tr_b16.  Two LDS buffers per operand.  V rows past the end of
 // the cache or in a missing page load as zeros (the buffer load is bounded to
 // the page's valid tokens), so a masked key contributes exactly 0 even if the
-// page holds NaN bits.
+// page holds NaN bits.  Each wave also has an LDS area of its own through
+// which its finished rows leave as whole rows (128 KB of LDS in all, one
+// workgroup per CU).
 #include "kvc_common.h"
 
 #include <algorithm>
@@ -108,8 +110,6 @@ struct alignas(16) VTile { uint8_t b[kKeys * kKRow]; };
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Two floats as a bf16 pair (v_cvt_pk_bf16_f32: round to nearest even).
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
@@ -537,9 +537,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
       const int t_head = G <= 4 ? 0 : 4 * t % G;
       const uint4 v = *reinterpret_cast<const uint4*>(rd + 4 * t * kORow);
       if (t_tok + lane_tok < toks_left)
-        __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w},
-                                    reinterpret_cast<u32x4*>(obase + int64_t(t_tok) * a.out_stride +
-                                                             t_head * kD));
+        store_stream(obase + int64_t(t_tok) * a.out_stride + t_head * kD, v);
       __builtin_amdgcn_sched_barrier(0);
     }
     if (row_ok && a.lse && half == 0)
