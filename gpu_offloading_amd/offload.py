@@ -78,9 +78,7 @@ class SwapPreemption:
     def preempt(self, slot: int, key, host=None) -> SwapHandle:
         """Swap ``slot`` out under ``key``.  ``host``: an optional pinned host
         buffer to hold the image (``PagedKVCache.swap_out``); an engine that
-        keeps a pool of them avoids pinning a new buffer per preemption, and
-        the first copies through a newly pinned buffer run well below the
-        link rate."""
+        keeps a pool of them avoids pinning a new buffer per preemption."""
         if key in self._swapped:
             raise RuntimeError(f"request {key!r} is already swapped out")
         handle = self.cache.swap_out([slot], host=host)
