@@ -203,6 +203,28 @@ def test_prefill_strided_q_and_out(gpu):
     assert (outbig[:, :4] == 7).all() and (outbig[:, 36:] == 7).all()
 
 
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_prefill_writes_only_its_rows(gpu, group):
+    """The output rows leave as whole rows, four per store, masked past each
+    request's last query: every row and head of a larger buffer outside the
+    batch's rows keeps its contents, and every row inside is written (the
+    sentinel value 7 appears nowhere in it)."""
+    hkv = 8 // group if group < 8 else 1
+    hq = hkv * group
+    q_lens = [37, 5, 70]       # partial query tiles of every group size
+    q, kc, vc, qo, kvi, idx, lpl = _case(q_lens, [300, 40, 70], hq, hkv, 23, device=gpu)
+    n = q.shape[0]
+    outbig = torch.full((n + 40, hq + 2, 128), 7.0, dtype=torch.bfloat16, device=gpu)
+    out = outbig[3:3 + n, 1:1 + hq]
+    (res, _), _ = _run(gpu, q, kc, vc, qo, kvi, idx, lpl, hq, hkv, out=out)
+    ref, _ = orc.paged_prefill(u16(q), u16(kc), u16(vc), qo, kvi, idx, lpl)
+    assert_attn_close(res.float().cpu().numpy(), ref)
+    big = outbig.cpu()
+    assert (big[:3] == 7).all() and (big[3 + n:] == 7).all()
+    assert (big[:, 0] == 7).all() and (big[:, 1 + hq:] == 7).all()
+    assert not (big[3:3 + n, 1:1 + hq] == 7).all(dim=-1).any()
+
+
 def test_prefill_rejects_unsupported(gpu):
     w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(WS, dtype=torch.uint8, device=gpu))
     i = torch.tensor([0, 4], dtype=torch.int32)
