@@ -712,10 +712,11 @@ __global__ __launch_bounds__(64 * kSmallWaves) void decode_small_kernel(DecodeAr
       acc[g][1] *= al;
     }
     wave_lds_fence();
-    // p.v over the page's 16 rows (rows past `valid` are zero).
+    // p.v over the page's rows: all 16 for a full page, else four at a time
+    // up to `valid` (rows past it have p = 0 and zero V rows, so leaving
+    // them out changes nothing).
     const uint32_t* vcol = reinterpret_cast<const uint32_t*>(tile.v) + lane;
-#pragma unroll
-    for (int tt = 0; tt < kPage; ++tt) {
+    auto pv_row = [&](int tt) {
       const uint32_t vw = vcol[tt * Tile::kRowChunks * 4];
       const float v0 = bf16lo(vw);
       const float v1 = bf16hi(vw);
@@ -724,6 +725,15 @@ __global__ __launch_bounds__(64 * kSmallWaves) void decode_small_kernel(DecodeAr
         const float pg = p_buf[tt * G + g];
         acc[g][0] = fmaf(pg, v0, acc[g][0]);
         acc[g][1] = fmaf(pg, v1, acc[g][1]);
+      }
+    };
+    if (valid == kPage) {
+#pragma unroll
+      for (int tt = 0; tt < kPage; ++tt) pv_row(tt);
+    } else {
+      for (int t4 = 0; t4 < valid; t4 += 4) {
+#pragma unroll
+        for (int tt = t4; tt < t4 + 4; ++tt) pv_row(tt);
       }
     }
     wave_lds_fence();  // the tile and p_buf are rewritten by the next page
