@@ -201,11 +201,13 @@ def test_decode_empty_requests_when_no_request_is_split(gpu, lens):
 def test_decode_small_batch_kernel(gpu, group):
     """Small-batch schedules (one workgroup per request and KV head, the
     waves' states merged in LDS): against the oracle and fp32 SDPA, empty
-    requests zero / -inf, rows past each request's end poisoned with NaN."""
+    requests zero / -inf, rows past each request's end poisoned with NaN.
+    The last pages hold 1, 3, 4, 5, 8, 13, 15 and 16 rows (p.v stops at the
+    first multiple of four past a partial page's rows)."""
     print(f"decode small-batch kernel, group {group}", flush=True)
     hkv = 8 if group <= 4 else 4
     hq = hkv * group
-    lens = [129, 1, 0, 256, 17, 16, 100]
+    lens = [129, 1, 0, 256, 17, 16, 100, 21, 24, 45, 47, 3]
     kc, vc, bt, indptr, indices, lpl = _paged(lens, hkv, 128, 26 + group)
     for b, ln in enumerate(lens):
         if ln % 16:
