@@ -160,6 +160,57 @@ def test_decode_group_sizes_and_head_dims(gpu, group, d):
     assert_attn_close(out.float().cpu().numpy(), ref)
 
 
+def test_decode_random_shapes(gpu):
+    """Seeded random batches against the oracle (output and lse): batch
+    sizes 1-48; lengths mixing empty requests, one-page requests, exact
+    page multiples and long contexts; group sizes 1-8; head dims 64 / 128 /
+    256; 1-8 KV heads; planner-chosen and forced segment counts.  The last
+    twelve cases use 8 KV heads of 128 dims (the streaming kernel's
+    eight-head workgroups), the last six with requests of at most 16 pages
+    (the small-batch kernel).  Lengths are scaled down so that each cache
+    stays under 16M elements."""
+    rng = np.random.default_rng(31)
+    combos = [(1, 128), (2, 128), (4, 128), (8, 128), (1, 64), (4, 64), (8, 64),
+              (1, 256), (2, 256), (4, 256)]
+    for case in range(36):
+        if case < 24:
+            group, d = combos[int(rng.integers(len(combos)))]
+            hkv = int(rng.choice([1, 2, 4, 8]))
+        else:  # the Mixtral-shaped kernels: 8 KV heads of 128 dims
+            group, d, hkv = int(rng.choice([1, 2, 4])), 128, 8
+        hq = hkv * group
+        short = case >= 30  # at most 16 pages per request: the small-batch kernel
+        b = int(rng.integers(1, 17 if short else 49))
+        kind = rng.random(b)
+        lens = np.where(kind < 0.1, 0,
+                        np.where(kind < 0.3, rng.integers(1, 17, b),
+                                 np.where(kind < 0.5, 16 * rng.integers(1, 17 if short else 20, b),
+                                          rng.integers(17, 257 if short else 2500, b))))
+        cap = (16 << 20) // (hkv * d)
+        while lens.sum() > cap:
+            lens = np.where(lens > 16, lens // 2, lens)
+        lens = [int(x) for x in lens]
+        segs = None if short else [None, None, 1, int(rng.integers(2, 600))][int(rng.integers(4))]
+        print(f"decode random case {case}: B={b} G={group} D={d} Hkv={hkv} segs={segs} "
+              f"tokens={sum(lens)}", flush=True)
+        kc, vc, bt, indptr, indices, lpl = _paged(lens, hkv, d, 100 + case)
+        q = randn_bf16((b, hq, d), 200 + case, device=gpu)
+        (out, lse), w = _run(gpu, q, kc.to(gpu), vc.to(gpu), indptr, indices, lpl, hq, hkv, d,
+                             segs=segs)
+        if short and sum(lens):
+            assert w.schedule.small_batch == 1
+        ref, ref_lse = orc.paged_decode(u16(q), u16(kc), u16(vc), indptr, indices, lpl)
+        assert_attn_close(out.float().cpu().numpy(), ref)
+        got_lse = lse.cpu().numpy()
+        live = [i for i, ln in enumerate(lens) if ln]
+        empty = [i for i, ln in enumerate(lens) if not ln]
+        if live:
+            assert np.allclose(got_lse[live], ref_lse[live], atol=1e-3, rtol=1e-4)
+        if empty:
+            assert np.isneginf(got_lse[empty]).all()
+            assert int(out[empty].abs().sum()) == 0
+
+
 def test_decode_empty_request_gives_zero_and_neg_inf_lse(gpu):
     lens = [0, 40, 0]
     kc, vc, bt, indptr, indices, lpl = _paged([40], 8, 128, 10)
