@@ -85,6 +85,33 @@ def test_prefill_edge_cases(gpu):
     _check(gpu, [0, 20, 6, 0, 9], [12, 5, 0, 17, 40], 32, 8, 34)
 
 
+def test_prefill_random_shapes(gpu):
+    """Seeded random batches against the oracle (output and lse): 1-8
+    requests, group sizes 1-8, 1-8 KV heads, causal and not; caches of
+    0-2500 tokens (some exact page multiples), chunks shorter than, equal to
+    or (a few) longer than their cache, empty chunks.  Sizes are scaled down
+    so that the oracle's q_len x kv_len x Hq stays under 6e7 per case."""
+    rng = np.random.default_rng(47)
+    for case in range(20):
+        group = int(rng.choice([1, 2, 4, 8]))
+        hkv = int(rng.choice([1, 2, 4, 8]))
+        hq = hkv * group
+        b = int(rng.integers(1, 9))
+        kv = np.where(rng.random(b) < 0.2, 16 * rng.integers(0, 40, b), rng.integers(0, 2500, b))
+        ql = np.minimum(kv, rng.integers(0, 700, b))
+        ql = np.where(rng.random(b) < 0.1, kv + rng.integers(1, 20, b), ql)
+        ql = np.where(rng.random(b) < 0.1, 0, ql)
+        if ql.sum() == 0:
+            ql[0] = 1
+        while int((ql * kv).sum()) * hq > 60_000_000:
+            kv, ql = (kv + 1) // 2, (ql + 1) // 2
+        causal = bool(rng.random() < 0.8)
+        q_lens, kv_lens = [int(x) for x in ql], [int(x) for x in kv]
+        print(f"prefill random case {case}: G={group} Hkv={hkv} causal={causal} "
+              f"q={q_lens} kv={kv_lens}", flush=True)
+        _check(gpu, q_lens, kv_lens, hq, hkv, 300 + case, causal=causal)
+
+
 @pytest.mark.parametrize("q_len,kv_len", [(37, 37), (37, 1000), (130, 1000)])
 def test_prefill_nan_past_the_end(gpu, q_len, kv_len):
     """Tokens of the last page past kv_len hold NaN bits; they must not leak.
