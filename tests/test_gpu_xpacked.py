@@ -134,6 +134,43 @@ def test_xpacked_v1_and_gqa(gpu, dt, group):
     assert_attn_close(out2.float().cpu().numpy(), ref)
 
 
+def test_xpacked_random_shapes(gpu):
+    """Seeded random batches, v1 and v2 against the oracle: fp16 / bf16,
+    group sizes 1-8, 1-16 KV heads, 1-20 sequences of 0-3000 tokens (empty
+    ones give zeros), and v2 launched with a max_seq_len up to 1500 tokens
+    past the longest sequence (partitions no sequence reaches)."""
+    rng = np.random.default_rng(53)
+    for case in range(16):
+        dt = ["fp16", "bf16"][case % 2]
+        group = int(rng.choice([1, 2, 4, 8]))
+        hkv = int(rng.choice([1, 2, 4, 8, 16]))
+        b = int(rng.integers(1, 21))
+        lens = np.where(rng.random(b) < 0.1, 0, rng.integers(1, 3001, b))
+        while int(lens.sum()) * hkv > 400_000:
+            lens = (lens + 1) // 2
+        lens = [int(x) for x in lens]
+        scale = float(rng.uniform(0.03, 0.12))
+        extra = int(rng.integers(0, 1501))
+        print(f"xpacked random case {case}: {dt} G={group} Hkv={hkv} lens={lens} extra={extra}",
+              flush=True)
+        q, kc, vc, bt = _attn_case(lens, hkv * group, hkv, dt, 400 + case, gpu)
+        ref, *_ = orc.paged_attention_xpacked(u16(q), u16(kc), u16(vc), bt, np.array(lens), scale,
+                                              dtype=dt)
+        live = [i for i, n in enumerate(lens) if n]
+        empty = [i for i, n in enumerate(lens) if not n]
+        out1 = torch.empty_like(q)
+        ops.paged_attention_v1(out1, q, kc, vc, hkv, scale, torch.from_numpy(bt).to(gpu),
+                               torch.tensor(lens, dtype=torch.int32, device=gpu), 16,
+                               max(max(lens), 1), None, "auto", 1.0, 1.0)
+        out2, *_ = _run_v2(q, kc, vc, bt, lens, hkv, scale, gpu,
+                           max_seq_len=max(max(lens), 1) + extra)
+        for out in (out1, out2):
+            if live:
+                assert_attn_close(out[live].float().cpu().numpy(), ref[live])
+            if empty:
+                assert (out[empty] == 0).all()
+
+
 def test_xpacked_empty_sequence_and_nan_past_the_end(gpu):
     lens = [0, 37, 600]
     q, kc, vc, bt = _attn_case(lens, 8, 8, "fp16", 64, gpu)
