@@ -938,10 +938,11 @@ def run_cfg5(torch, seed, decode_steps=6):
     npages = sum(cache.seq_pages(s) for s in victims)
     host = hostmem.pinned_empty(L * npages * bb, "cuda")
     nbytes_est = L * npages * bb
-    # One untimed eviction and restore of the same victims first: the first
-    # swaps of a process pay one-time runtime costs on the host (measured
-    # 19.7 / 9.9 / 3.6 ms to enqueue the first three swap-outs), reported
-    # here apart from the steady-state figure below.
+    # One untimed eviction and restore of the same victims first, reported
+    # apart from the steady-state figure below.  Without reserve_swap's
+    # warm-up of the runtime's copy path the first swaps of a process paid
+    # one-time host costs (18-31 / 10-16 / 3 ms to enqueue the first three
+    # swap-outs); with it the first is within a few ms of the later ones.
     t0 = time.perf_counter()
     hw = cache.swap_out(victims, host=host)
     first_out_ms = (time.perf_counter() - t0) * 1e3

@@ -165,6 +165,7 @@ class PagedKVCache:
         self._staging_free: list[Optional[torch.cuda.Event]] = [None, None]
         self._swap_stream: Optional[torch.cuda.Stream] = None
         self._copy_stream: Optional[torch.cuda.Stream] = None
+        self._swap_warm = False   # reserve_swap's copy-path warm-up done
         self._swaps = SwapLedger()   # swap-outs / restores still in flight
 
     def _init_step_buffers(self) -> None:
@@ -952,16 +953,65 @@ class PagedKVCache:
             self._staging = torch.empty(self._staging_bytes, dtype=torch.uint8, device=self.device)
         return self._staging
 
+    # Round trips of the swap warm-up: at least a large eviction's chunk count
+    # (an 8.6 GB swap through 256 MiB staging halves makes 32 copies).
+    _SWAP_WARM_COPIES = 32
+    _SWAP_WARM_BYTES = 16 << 20
+
     def reserve_swap(self) -> None:
         """Allocate the swap staging buffer and create the side and DMA
         streams now, so that the first ``swap_out`` does not pay for them on
         the engine loop (a 512 MiB device allocation and two stream creations
         take ~17 ms of host time).  Without this call they are made on the
-        first swap."""
+        first swap.
+
+        The first call also warms the runtime's copy path: 32 round trips of
+        a 16 MiB pinned buffer through the staging on the DMA stream, ordered
+        by events as a swap's chunks are, and a gather of block 0 of every
+        layer into the staging on the side stream (it reads the caches and
+        writes only the staging).  A process's first few dozen such copies
+        and stream waits cost the host far more than later ones: the first
+        8.6 GB swap-out (32 chunks) took 18-31 ms to enqueue without the
+        warm-up and 3 ms after it; copies of 64 KB, or fewer round trips,
+        left 5-15 ms.  The warm-up takes ~25 ms and waits for it to finish."""
         self._require_gpu()
-        self._staging_buf()
-        self._side_stream()
-        self._dma_stream()
+        st = self._staging_buf()
+        side, dma = self._side_stream(), self._dma_stream()
+        if self._swap_warm:
+            return
+        # Work already enqueued on the current stream (which the staging's
+        # memory may still serve) and earlier swaps' staging use (kernels on
+        # one stream, copies on the other) finish before the warm-up
+        # overwrites the staging.
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        side.wait_stream(dma)
+        dma.wait_stream(side)
+        nb = min(self._SWAP_WARM_BYTES, st.numel())
+        host = hostmem.pinned_empty(nb, self.device)
+        for _ in range(self._SWAP_WARM_COPIES):
+            e = torch.cuda.Event()
+            e.record(side)
+            dma.wait_event(e)
+            with torch.cuda.stream(dma):
+                host.copy_(st[:nb], non_blocking=True)
+            e = torch.cuda.Event()
+            e.record(dma)
+            side.wait_event(e)
+            with torch.cuda.stream(dma):
+                st[:nb].copy_(host, non_blocking=True)
+            e = torch.cuda.Event()
+            e.record(dma)
+            side.wait_event(e)
+        per = 2 * ops.block_bytes(self.k_cache[0])
+        if per <= st.numel():
+            with torch.cuda.stream(side):
+                ids0 = torch.zeros(1, dtype=torch.int32, device=self.device)
+            for layer in range(self.num_layers):
+                ops.gather_blocks(self.k_cache[layer], self.v_cache[layer], ids0, st[:per],
+                                  stream=side)
+        side.synchronize()
+        dma.synchronize()
+        self._swap_warm = True
 
     def _staging_halves(self, per_block: int):
         """The staging buffer as two halves and the blocks one half holds."""

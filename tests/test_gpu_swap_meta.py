@@ -174,6 +174,40 @@ def test_cache_swap_chunks_across_layers_bit_exact(gpu, staging_blocks):
     assert [int(cache._seq_lens_cpu[s]) for s in (3, 0, 1, 2)] == [70, 64, 40, 0]
 
 
+@pytest.mark.parametrize("staging_blocks", [1, 1000])
+def test_reserve_swap_warm_up_leaves_the_caches_untouched(gpu, staging_blocks):
+    """reserve_swap's warm-up (copies through the staging, gathers of block 0
+    into it) changes no cache byte, runs once, and a swap round trip after
+    it is exact; staging of 2 blocks (smaller than the warm-up's 16 MiB
+    copies) and of 2000 blocks."""
+    from gpu_offloading_amd.kv_cache import PagedKVCache
+
+    layers, hkv = 3, 2
+    per = 2 * 16 * hkv * 128 * 2
+    cache = PagedKVCache(layers, hkv, 128, max_seqs=2, max_seq_len=256, kv_page_budget=32,
+                         free_page_order=workloads.randperm(32, 90), device=gpu,
+                         workspace_bytes=1 << 20, staging_bytes=2 * staging_blocks * per)
+    cache.ensure_pages(0, 5)
+    cache.advance([0], [70])
+    cache.fill_kv_random(1.0, generator=torch.Generator(device=gpu).manual_seed(91))
+    snap = cache.kv_snapshot()
+    cache.reserve_swap()
+    cache.reserve_swap()
+    torch.cuda.synchronize()
+    for l in range(layers):
+        assert torch.equal(cache.k_cache[l], snap[0][l])
+        assert torch.equal(cache.v_cache[l], snap[1][l])
+    pages = cache.block_table.cpu().numpy()[0, :5].copy()
+    h = cache.swap_out([0])
+    cache.swap_in(h, wait=True)
+    torch.cuda.synchronize()
+    dst = torch.from_numpy(cache.block_table.cpu().numpy()[0, :5]).long().to(gpu)
+    src = torch.from_numpy(pages).long().to(gpu)
+    for l in range(layers):
+        assert torch.equal(cache.k_cache[l][dst], snap[0][l][src])
+        assert torch.equal(cache.v_cache[l][dst], snap[1][l][src])
+
+
 def test_cfg5_swap_under_decode_round_trip(gpu):
     """Configuration 5's shape (OLMoE MHA 16 x 128, 128 requests x 2048
     tokens on a shuffled 16,384-page pool; 4 of its 16 layers): a seeded
