@@ -196,17 +196,19 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
                 rfl(t.y.x), rfl(t.y.y), rfl(t.y.z), rfl(t.y.w)};
   };
   // Q of a unit as the B operand of S^T = K Q^T: k-step ks covers head dims
-  // 16ks .. 16ks+15, lane half h the dims 16ks + 8h .. +7.
+  // 16ks .. 16ks+15, lane half h the dims 16ks + 8h .. +7.  Rows past the
+  // chunk load the chunk's first token (every unit has one): a row's scores,
+  // softmax and output involve only its own Q, and such rows are never
+  // stored.  Every lane loads, so the loads need no branches around them
+  // and the compiler can count them exactly (branches made it wait for all
+  // loads in flight, these included, at the unit switch).
   auto load_q = [&](const Unit& U, bf16x8_t (&dst)[kD / 16]) __attribute__((always_inline)) {
     const int t = U.tok0 + wave * kTokPerWave + r / G;
-    const bool ok = t < U.q_len;
-    const uint16_t* qp = a.q + int64_t(U.q_off + (ok ? t : 0)) * a.q_stride +
+    const uint16_t* qp = a.q + int64_t(U.q_off + (t < U.q_len ? t : 0)) * a.q_stride +
                          int64_t(U.h * G + g) * kD + 8 * half;
 #pragma unroll
-    for (int ks = 0; ks < kD / 16; ++ks) {
-      const uint4 v = ok ? *reinterpret_cast<const uint4*>(qp + 16 * ks) : make_uint4(0, 0, 0, 0);
-      dst[ks] = as_bf16x8(v);
-    }
+    for (int ks = 0; ks < kD / 16; ++ks)
+      dst[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 16 * ks));
   };
 
   // The current unit and this lane's row in it.
@@ -531,13 +533,22 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs a
     uint16_t* obase = a.out + int64_t(cu.q_off + wave_tok + lane_tok) * a.out_stride +
                       int64_t(cu.h * G + lane_head) * kD + 8 * c;
     const uint8_t* rd = stg + q * kORow + 16 * c;
+    // Four read-backs in flight, then their four stores (one at a time, each
+    // store waited for its own read).
 #pragma unroll
-    for (int t = 0; t < kWaveRows / 4; ++t) {
-      const int t_tok = G <= 4 ? t * (4 / G) : 4 * t / G;
-      const int t_head = G <= 4 ? 0 : 4 * t % G;
-      const uint4 v = *reinterpret_cast<const uint4*>(rd + 4 * t * kORow);
-      if (t_tok + lane_tok < toks_left)
-        store_stream(obase + int64_t(t_tok) * a.out_stride + t_head * kD, v);
+    for (int t0 = 0; t0 < kWaveRows / 4; t0 += 4) {
+      uint4 v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[i] = *reinterpret_cast<const uint4*>(rd + 4 * (t0 + i) * kORow);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + i;
+        const int t_tok = G <= 4 ? t * (4 / G) : 4 * t / G;
+        const int t_head = G <= 4 ? 0 : 4 * t % G;
+        if (t_tok + lane_tok < toks_left)
+          store_stream(obase + int64_t(t_tok) * a.out_stride + t_head * kD, v[i]);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     if (row_ok && a.lse && half == 0)
